@@ -1,0 +1,325 @@
+#!/usr/bin/env python3
+"""Benchmark of hetero-serve's paged-attention hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps 50] [--warmup 5] [--config C2]
+
+One step is one call of the decode attention (hs_decode: the partition
+kernel plus the log-sum-exp merge) over one layer of the whole batch, with
+every input already resident in HBM.  The headline workload is configuration
+C2 (ragged decode, batch 64, 32 heads, head_dim 128, bf16 KV, block_size 16,
+context lognormal(median 2048, sigma 0.8) clipped to [64, 8192]); `value` is
+its algorithmic HBM throughput in GB/s (K and V of every context token read
+once, divided by the step time).  The JSON line also carries:
+
+  roofline      the partition kernel alone, timed with HIP events that the
+                library records around that launch on its own stream, against
+                MI355X's 8 TB/s HBM peak
+  cpu_baseline  the CPU oracle (oracle/attention.py) timed on this host on a
+                seeded sample of C2's sequences
+  secondary     chunked prefill (C4) in TFLOP/s against the dense fp16 MFMA
+                peak, and the 4096-block migration pack of C5 in GB/s
+
+Only rank 0 of a one-GPU run exists: there is no multi-GPU path on this box.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT, ROOT / "hetero-serve_amd"):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+METRIC = "decode µs/step + HBM GB/s (% peak); prefill TFLOP/s (% MFMA peak)"
+HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0
+
+
+def log(*a) -> None:
+    print(*a, file=sys.stderr, flush=True)
+
+
+# ---------------------------------------------------------------------------
+# GPU legs
+# ---------------------------------------------------------------------------
+
+
+def decode_leg(case, steps: int, warmup: int, partition_tokens: int = 0) -> dict:
+    """Time hs_decode on `case`; returns step/kernel times and throughputs."""
+    import torch
+
+    from heteroserve import _hip
+    from hsbench.timing import time_steps
+
+    lib = _hip.lib()
+    B, H, D = case.q.shape
+    kc, vc = case.k_cache, case.v_cache
+    NB, BS, Hkv, _ = kc.shape
+    MB = case.block_tables.shape[1]
+    out = torch.empty((B, H, D), dtype=torch.float32, device=case.q.device)
+    ws_bytes = lib.hs_decode_workspace_bytes(B, H, D, BS, MB, 0, partition_tokens)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=case.q.device)
+    stream = torch.cuda.current_stream().cuda_stream
+    dt = _hip.dtype_code(kc.dtype)
+    args = (case.q.data_ptr(), kc.data_ptr(), vc.data_ptr(), dt, NB,
+            case.block_tables.data_ptr(), case.context_lens.data_ptr(), out.data_ptr(),
+            B, H, Hkv, D, BS, MB, float(case.scale), 0, partition_tokens, ws.data_ptr(),
+            ws_bytes, stream)
+
+    def step():
+        _hip.check(lib.hs_decode(*args))
+
+    def arm(s, e):
+        _hip.check(lib.hs_profile_next_launch(s.handle, e.handle))
+
+    step_ms, kernel_ms, wall = time_steps(step, steps, warmup, stream, arm)
+    nbytes = case.decode_bytes()
+    k_ms = statistics.mean(kernel_ms)
+    return dict(step_ms=step_ms, kernel_ms=k_ms, kernel_ms_min=min(kernel_ms), wall_s=wall,
+                bytes=nbytes, step_gbs=nbytes / (step_ms * 1e-3) / 1e9,
+                kernel_gbs=nbytes / (k_ms * 1e-3) / 1e9, out=out)
+
+
+def prefill_leg(case, steps: int, warmup: int) -> dict:
+    import torch
+
+    from heteroserve import _hip
+    from hsbench.timing import time_steps
+
+    lib = _hip.lib()
+    T, H, D = case.q.shape
+    kc, vc = case.k_cache, case.v_cache
+    NB, BS, Hkv, _ = kc.shape
+    B, MB = case.block_tables.shape
+    out = torch.empty((T, H, D), dtype=torch.float32, device=case.q.device)
+    stream = torch.cuda.current_stream().cuda_stream
+    args = (case.q.data_ptr(), case.cu_seqlens.data_ptr(), int(case.q_lens.max()),
+            kc.data_ptr(), vc.data_ptr(), _hip.dtype_code(kc.dtype), NB,
+            case.block_tables.data_ptr(), case.context_lens.data_ptr(), out.data_ptr(),
+            B, H, Hkv, D, BS, MB, float(case.scale), 1, stream)
+
+    def step():
+        _hip.check(lib.hs_prefill_varlen(*args))
+
+    def arm(s, e):
+        _hip.check(lib.hs_profile_next_launch(s.handle, e.handle))
+
+    step_ms, kernel_ms, wall = time_steps(step, steps, warmup, stream, arm)
+    flops = case.prefill_flops()
+    k_ms = statistics.mean(kernel_ms)
+    return dict(step_ms=step_ms, kernel_ms=k_ms, flops=flops,
+                step_tflops=flops / (step_ms * 1e-3) / 1e12,
+                kernel_tflops=flops / (k_ms * 1e-3) / 1e12)
+
+
+def pack_leg(steps: int, warmup: int) -> dict:
+    import torch
+
+    from heteroserve import _hip
+    from hsbench import cases
+    from hsbench.timing import time_steps
+
+    lib = _hip.lib()
+    nb = cases.C5_POOL_BLOCKS
+    dev = "cuda:0"
+    pool = torch.empty((1, 2, nb, 16, 32, 128), dtype=torch.bfloat16, device=dev)
+    cases._fill_pool(pool, torch.Generator(device=dev).manual_seed(41))
+    ids = torch.as_tensor(cases.c5_pack_ids(nb), dtype=torch.int64, device=dev)
+    out = torch.empty((ids.numel(), 1, 2, 16, 32, 128), dtype=torch.bfloat16, device=dev)
+    page = pool[0, 0, 0].numel() * pool.element_size()
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def step():
+        _hip.check(lib.hs_kv_pack(pool.data_ptr(), 1, nb, page, ids.data_ptr(), ids.numel(),
+                                  out.data_ptr(), stream))
+
+    def arm(s, e):
+        _hip.check(lib.hs_profile_next_launch(s.handle, e.handle))
+
+    step_ms, kernel_ms, _ = time_steps(step, steps, warmup, stream, arm)
+    want = pool[:, :, ids].permute(2, 0, 1, 3, 4, 5)
+    exact = bool(torch.equal(out.view(torch.int16), want.contiguous().view(torch.int16)))
+    nbytes = 2 * out.numel() * out.element_size()      # read + write
+    k_ms = statistics.mean(kernel_ms)
+    del pool, out, want
+    torch.cuda.empty_cache()
+    return dict(step_ms=step_ms, kernel_ms=k_ms, bytes=nbytes, bit_exact=exact,
+                kernel_gbs=nbytes / (k_ms * 1e-3) / 1e9, step_gbs=nbytes / (step_ms * 1e-3) / 1e9)
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline: the oracle on this host's cores
+# ---------------------------------------------------------------------------
+
+
+def cpu_baseline(case, n_seq: int = 16, seed: int = 7) -> dict:
+    """Per-sequence torch oracle on a seeded sample of the case's sequences."""
+    import numpy as np
+    import torch
+
+    from oracle.attention import decode_one
+
+    threads = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    rng = np.random.default_rng(seed)
+    pick = sorted(rng.choice(len(case.ctx), size=min(n_seq, len(case.ctx)), replace=False))
+    host = []
+    for b in pick:
+        n = int(case.ctx[b])
+        nblk = -(-n // 16)
+        blocks = case.block_tables[b, :nblk].long()
+        host.append((case.q[b].cpu(), case.k_cache.index_select(0, blocks).cpu(),
+                     case.v_cache.index_select(0, blocks).cpu(),
+                     torch.arange(nblk, dtype=torch.int32), n))
+    total = 0.0
+    for q, kb, vb, tbl, n in host:
+        decode_one(q, kb, vb, tbl, n, case.scale)           # warm-up
+        runs = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            decode_one(q, kb, vb, tbl, n, case.scale)
+            runs.append(time.perf_counter() - t0)
+        total += statistics.median(runs)
+    tokens = int(sum(int(case.ctx[b]) for b in pick))
+    nbytes = tokens * case.row_bytes()
+    return {
+        "value": round(nbytes / total / 1e9, 3),
+        "unit": "GB/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"{len(pick)} seeded {case.name} sequences ({tokens} of "
+                   f"{int(case.ctx.sum())} context tokens), oracle/attention.py decode_one "
+                   f"(torch fp32 CPU), median of 3 after 1 warm-up, summed: "
+                   f"{total * 1e3:.1f} ms for {nbytes / 1e6:.1f} MB of K+V; "
+                   f"cpu={platform.processor() or platform.machine()}"),
+    }
+
+
+# ---------------------------------------------------------------------------
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="C2", choices=["C1", "C2", "C3", "C5-decode"],
+                    help="decode configuration of the headline line")
+    ap.add_argument("--partition", type=int, default=0,
+                    help="decode partition tokens (0 = library default)")
+    ap.add_argument("--no-secondary", action="store_true", help="skip the C4 / C5 pack legs")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        log(f"bench.py runs on exactly one GPU; --gpus {args.gpus} is not supported "
+            "(the paged-attention path has no multi-GPU decomposition on this box).")
+        return 2
+
+    import torch
+
+    from heteroserve import _hip
+    from hsbench import cases
+
+    if not _hip.ready():
+        log(f"libhsattn unavailable: {_hip.error()}")
+        return 1
+    dev = "cuda:0"
+    log(f"device: {torch.cuda.get_device_name(0)}")
+
+    case = cases.CONFIGS[args.config](dev)
+    log(f"{case.name}: B={len(case.ctx)} sum(ctx)={int(case.ctx.sum())} "
+        f"bytes={case.decode_bytes() / 1e9:.3f} GB")
+    dec = decode_leg(case, args.steps, args.warmup, args.partition)
+    log(f"decode: step {dec['step_ms'] * 1e3:.1f} us ({dec['step_gbs']:.0f} GB/s), "
+        f"partition kernel {dec['kernel_ms'] * 1e3:.1f} us ({dec['kernel_gbs']:.0f} GB/s)")
+
+    cpu = None if args.no_cpu else cpu_baseline(case)
+    if cpu:
+        log(f"cpu baseline: {cpu['value']} GB/s on {cpu['cores']} threads")
+
+    kv_dtype = str(case.k_cache.dtype).replace("torch.", "")
+    config = {
+        "workload": f"{case.name} paged decode, one layer",
+        "batch": len(case.ctx), "heads": case.n_heads, "kv_heads": case.kv_heads,
+        "head_dim": case.head_dim, "block_size": 16, "kv_dtype": kv_dtype,
+        "sum_context": int(case.ctx.sum()), "max_context": int(case.ctx.max()),
+        "num_blocks": int(case.k_cache.shape[0]),
+        "decomposition": f"fixed partitions of {args.partition or 256} tokens + LSE merge",
+        "parallelism": "none (one GPU)",
+    }
+    if case.meta.get("shared_blocks"):
+        config["unique_bytes"] = case.unique_decode_bytes()
+    del case
+    torch.cuda.empty_cache()
+
+    secondary = {}
+    if not args.no_secondary:
+        try:
+            pc = cases.c4_prefill(dev)
+            pre = prefill_leg(pc, max(5, args.steps // 5), 2)
+            secondary["C4_prefill"] = {
+                "us_per_step": round(pre["step_ms"] * 1e3, 2),
+                "tflops": round(pre["step_tflops"], 2),
+                "kernel_tflops": round(pre["kernel_tflops"], 2),
+                "mfma_frac": round(pre["kernel_tflops"] / MFMA_F16_PEAK_TFLOPS, 4),
+                "useful_flops": pre["flops"],
+            }
+            log(f"C4 prefill: {pre['step_ms'] * 1e3:.1f} us, {pre['kernel_tflops']:.1f} TFLOP/s")
+            del pc
+        except RuntimeError as exc:
+            secondary["C4_prefill"] = {"error": str(exc)[:200]}
+        torch.cuda.empty_cache()
+        pk = pack_leg(max(5, args.steps // 5), 2)
+        secondary["C5_pack"] = {
+            "us_per_step": round(pk["step_ms"] * 1e3, 2), "gbs": round(pk["kernel_gbs"], 1),
+            "hbm_frac": round(pk["kernel_gbs"] / HBM_PEAK_GBS, 4), "bit_exact": pk["bit_exact"],
+            "bytes_moved": pk["bytes"],
+        }
+        log(f"C5 pack: {pk['kernel_ms'] * 1e3:.1f} us, {pk['kernel_gbs']:.0f} GB/s, "
+            f"exact={pk['bit_exact']}")
+
+    line = {
+        "metric": METRIC,
+        "value": round(dec["step_gbs"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dec["step_ms"], 5),
+        "us_per_step": round(dec["step_ms"] * 1e3, 2),
+        "hbm_frac": round(dec["step_gbs"] / HBM_PEAK_GBS, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded N(0,1) KV and queries, seeded block tables)",
+        "config": config,
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "row_attn_part_kernel",
+            "achieved": round(dec["kernel_gbs"], 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(dec["kernel_gbs"] / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "algorithmic_bytes": dec["bytes"],
+            "kernel_us": round(dec["kernel_ms"] * 1e3, 2),
+        },
+        "cpu_baseline": cpu,
+        "secondary": secondary,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

@@ -1,0 +1,307 @@
+// extern "C" entry points of libhsattn.so (declared in include/hsattn.h).
+//
+// This layer validates arguments with the reference's error messages where it
+// has one, sizes grids and workspaces, and hands off to the kernel launchers.
+// It keeps no mutable state besides a per-device cache of CU counts and the
+// thread-local error message.
+#include <mutex>
+#include <string>
+#include <unordered_map>
+
+#include "hs_kernels.h"
+
+namespace hs {
+
+static thread_local std::string g_last_error;
+
+void set_error(const std::string& msg) { g_last_error = msg; }
+
+int fail(int code, const std::string& msg) {
+  g_last_error = msg;
+  return code;
+}
+
+int check_launch(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess)
+    return fail(HS_EHIP, std::string(what) + ": " + hipGetErrorString(e));
+  return HS_OK;
+}
+
+struct ProfileRequest {
+  hipEvent_t start = nullptr;
+  hipEvent_t stop = nullptr;
+};
+static thread_local ProfileRequest g_profile;
+
+// A failed record leaves the event unrecorded; the caller's elapsed-time
+// query then reports the error, so the status is not needed here.
+void profile_begin(hipStream_t stream) {
+  if (g_profile.start) (void)hipEventRecord(g_profile.start, stream);
+}
+
+void profile_end(hipStream_t stream) {
+  if (g_profile.stop) (void)hipEventRecord(g_profile.stop, stream);
+  g_profile = ProfileRequest{};
+}
+
+constexpr int kDefaultPartition = 256;
+
+static int device_cu_count(int device) {
+  static std::mutex mu;
+  static std::unordered_map<int, int> cache;
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = cache.find(device);
+  if (it != cache.end()) return it->second;
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
+    return -1;
+  cache[device] = cus;
+  return cus;
+}
+
+static bool valid_dtype(int t) {
+  return t == HS_DTYPE_F32 || t == HS_DTYPE_F16 || t == HS_DTYPE_BF16;
+}
+
+static bool valid_row_head_dim(int D) { return D == 32 || D == 64 || D == 128 || D == 256; }
+
+// Shared checks of the paged-attention entry points.
+static int check_attn_common(const void* q, const void* k, const void* v, int kv_dtype, int NB,
+                             const void* bt, const void* ctx, const void* out, int B, int H,
+                             int Hkv, int D, int BS, int MB) {
+  if (!q || !k || !v || !bt || !ctx || !out)
+    return fail(HS_EINVAL, "null tensor pointer");
+  if (!valid_dtype(kv_dtype))
+    return fail(HS_EINVAL, "unknown kv dtype code " + std::to_string(kv_dtype));
+  if (B < 0 || H <= 0 || Hkv <= 0 || D <= 0 || BS <= 0 || MB <= 0 || NB <= 0)
+    return fail(HS_EINVAL, "sizes must be positive");
+  if (H % Hkv != 0) return fail(HS_EINVAL, "n_head must be divisible by n_kv_head");
+  if (D % 32 != 0) return fail(HS_EINVAL, "head_dim must be a multiple of the warp size");
+  return HS_OK;
+}
+
+struct DecodePlan {
+  int mode, part_tokens, splits, P;
+};
+
+static int plan_decode(int BS, int MB, int num_splits, int partition_tokens, DecodePlan* plan) {
+  if (num_splits < 0) return fail(HS_EINVAL, "num_splits must be >= 0");
+  const int64_t max_ctx = (int64_t)MB * BS;
+  if (num_splits == 1) {
+    *plan = {0, 0, 1, 1};
+  } else if (num_splits > 1) {
+    *plan = {2, 0, num_splits, num_splits};
+  } else {
+    const int pt = partition_tokens > 0 ? partition_tokens : kDefaultPartition;
+    if (pt % 16 != 0) return fail(HS_EINVAL, "partition_tokens must be a multiple of 16");
+    const int64_t P = (max_ctx + pt - 1) / pt;
+    *plan = {P <= 1 ? 0 : 1, pt, 0, (int)(P < 1 ? 1 : P)};
+  }
+  return HS_OK;
+}
+
+static size_t decode_ws_bytes(int64_t rows, int H, int D, int P) {
+  if (P <= 1) return 0;
+  const size_t acc = (size_t)rows * H * P * D * sizeof(float);
+  const size_t acc_aligned = (acc + 255) & ~(size_t)255;
+  return acc_aligned + (size_t)rows * H * P * 2 * sizeof(float);
+}
+
+}  // namespace hs
+
+using namespace hs;
+
+extern "C" {
+
+int hs_abi_version(void) { return HS_ABI_VERSION; }
+
+const char* hs_last_error(void) { return g_last_error.c_str(); }
+
+int hs_device_cu_count(int device) { return device_cu_count(device); }
+
+int hs_profile_next_launch(void* start_event, void* stop_event) {
+  if ((start_event == nullptr) != (stop_event == nullptr))
+    return fail(HS_EINVAL, "pass both events or neither");
+  g_profile.start = static_cast<hipEvent_t>(start_event);
+  g_profile.stop = static_cast<hipEvent_t>(stop_event);
+  return HS_OK;
+}
+
+int64_t hs_choose_num_splits(int64_t num_seqs, int64_t num_heads, int64_t max_context) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    set_error("hipGetDevice failed");
+    return -1;
+  }
+  const int sms = device_cu_count(dev);
+  if (sms <= 0) {
+    set_error("could not read the device CU count");
+    return -1;
+  }
+  // paged_attn_v3.py:224-231
+  const int64_t have = num_seqs * num_heads > 1 ? num_seqs * num_heads : 1;
+  const int64_t by_chain = max_context / 32 > 1 ? max_context / 32 : 1;
+  const int64_t fill = ((int64_t)sms * 8 + have - 1) / have;
+  const int64_t to_fill = fill > 1 ? fill : 1;
+  int64_t s = by_chain > to_fill ? by_chain : to_fill;
+  s = s < 64 ? s : 64;
+  return s > 1 ? s : 1;
+}
+
+size_t hs_decode_workspace_bytes(int B, int H, int D, int BS, int MB, int num_splits,
+                                 int partition_tokens) {
+  DecodePlan plan;
+  if (B <= 0 || H <= 0 || D <= 0 || BS <= 0 || MB <= 0) return 0;
+  if (plan_decode(BS, MB, num_splits, partition_tokens, &plan) != HS_OK) return 0;
+  return decode_ws_bytes(B, H, D, plan.P);
+}
+
+int hs_decode(const float* q, const void* k_cache, const void* v_cache, int kv_dtype,
+              int num_blocks, const int32_t* block_tables, const int32_t* context_lens,
+              float* out, int B, int H, int Hkv, int D, int BS, int MB, float scale,
+              int num_splits, int partition_tokens, void* workspace, size_t workspace_bytes,
+              void* stream) {
+  int rc = check_attn_common(q, k_cache, v_cache, kv_dtype, num_blocks, block_tables,
+                             context_lens, out, B, H, Hkv, D, BS, MB);
+  if (rc != HS_OK) return rc;
+  if (!valid_row_head_dim(D))
+    return fail(HS_EUNSUPPORTED, "unsupported head_dim " + std::to_string(D));
+  if (B == 0) return HS_OK;
+  DecodePlan plan;
+  if ((rc = plan_decode(BS, MB, num_splits, partition_tokens, &plan)) != HS_OK) return rc;
+  const size_t need = decode_ws_bytes(B, H, D, plan.P);
+  if (need > 0 && (!workspace || workspace_bytes < need))
+    return fail(HS_EWORKSPACE, "decode needs " + std::to_string(need) + " workspace bytes, got " +
+                                   std::to_string(workspace ? workspace_bytes : 0));
+  RowAttnArgs a{};
+  a.q = q;
+  a.k = k_cache;
+  a.v = v_cache;
+  a.bt = block_tables;
+  a.ctx = context_lens;
+  a.cu_q = nullptr;
+  a.out = out;
+  a.part_acc = static_cast<float*>(workspace);
+  const size_t acc_bytes = ((size_t)B * H * plan.P * D * sizeof(float) + 255) & ~(size_t)255;
+  a.part_ml = need ? reinterpret_cast<float*>(static_cast<char*>(workspace) + acc_bytes) : nullptr;
+  a.rows = B;
+  a.S = 1;
+  a.B = B;
+  a.H = H;
+  a.Hkv = Hkv;
+  a.BS = BS;
+  a.MB = MB;
+  a.NB = num_blocks;
+  a.mode = plan.mode;
+  a.part_tokens = plan.part_tokens;
+  a.splits = plan.splits;
+  a.P = plan.P;
+  a.qscale = scale * kLog2e;
+  return launch_row_attn(a, kv_dtype, D, static_cast<hipStream_t>(stream));
+}
+
+static int prefill_common(const float* q, const int32_t* cu_q, int S, int max_rows,
+                          const void* k_cache, const void* v_cache, int kv_dtype, int num_blocks,
+                          const int32_t* block_tables, const int32_t* context_lens, float* out,
+                          int B, int H, int Hkv, int D, int BS, int MB, float scale,
+                          int use_mfma, void* stream) {
+  int rc = check_attn_common(q, k_cache, v_cache, kv_dtype, num_blocks, block_tables,
+                             context_lens, out, B, H, Hkv, D, BS, MB);
+  if (rc != HS_OK) return rc;
+  if (S < 0 || max_rows < 0) return fail(HS_EINVAL, "query length must be >= 0");
+  if (B == 0 || max_rows == 0) return HS_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (use_mfma) {
+    if (kv_dtype != HS_DTYPE_F16 && kv_dtype != HS_DTYPE_BF16)
+      return fail(HS_EUNSUPPORTED, "the MFMA path needs an fp16 or bf16 KV cache");
+    if (BS != 16)
+      return fail(HS_EUNSUPPORTED, "the MFMA path needs block_size == 16 (one page per tile)");
+    if (!(D == 32 || D == 64 || D == 128))
+      return fail(HS_EUNSUPPORTED, "unsupported head_dim for the MFMA path: " + std::to_string(D));
+    return launch_prefill_mfma(q, cu_q, S, max_rows, k_cache, v_cache, kv_dtype, num_blocks,
+                               block_tables, context_lens, out, B, H, Hkv, D, BS, MB, scale, st);
+  }
+  if (!valid_row_head_dim(D))
+    return fail(HS_EUNSUPPORTED, "unsupported head_dim " + std::to_string(D));
+  RowAttnArgs a{};
+  a.q = q;
+  a.k = k_cache;
+  a.v = v_cache;
+  a.bt = block_tables;
+  a.ctx = context_lens;
+  a.cu_q = cu_q;
+  a.out = out;
+  a.rows = max_rows;
+  a.S = S;
+  a.B = B;
+  a.H = H;
+  a.Hkv = Hkv;
+  a.BS = BS;
+  a.MB = MB;
+  a.NB = num_blocks;
+  a.mode = 0;  // one pass per (row, head): no workspace
+  a.splits = 1;
+  a.P = 1;
+  a.qscale = scale * kLog2e;
+  return launch_row_attn(a, kv_dtype, D, st);
+}
+
+int hs_prefill(const float* q, const void* k_cache, const void* v_cache, int kv_dtype,
+               int num_blocks, const int32_t* block_tables, const int32_t* context_lens,
+               float* out, int B, int S, int H, int Hkv, int D, int BS, int MB, float scale,
+               int use_mfma, void* stream) {
+  if ((int64_t)B * S > 0x7fffffffLL) return fail(HS_EINVAL, "B * S too large");
+  return prefill_common(q, nullptr, S, B * S, k_cache, v_cache, kv_dtype, num_blocks,
+                        block_tables, context_lens, out, B, H, Hkv, D, BS, MB, scale, use_mfma,
+                        stream);
+}
+
+int hs_prefill_varlen(const float* q, const int32_t* cu_seqlens_q, int max_seqlen_q,
+                      const void* k_cache, const void* v_cache, int kv_dtype, int num_blocks,
+                      const int32_t* block_tables, const int32_t* context_lens, float* out,
+                      int B, int H, int Hkv, int D, int BS, int MB, float scale, int use_mfma,
+                      void* stream) {
+  if (!cu_seqlens_q) return fail(HS_EINVAL, "null cu_seqlens_q");
+  // Total rows are needed for the row grid; they are the last prefix sum,
+  // which lives on the device.  The caller passes max_seqlen_q, so the grid is
+  // sized B * max_seqlen_q and rows past a sequence's end exit early.
+  if ((int64_t)B * max_seqlen_q > 0x7fffffffLL) return fail(HS_EINVAL, "B * max_seqlen_q too large");
+  return prefill_common(q, cu_seqlens_q, max_seqlen_q, B * max_seqlen_q, k_cache, v_cache,
+                        kv_dtype, num_blocks, block_tables, context_lens, out, B, H, Hkv, D, BS,
+                        MB, scale, use_mfma, stream);
+}
+
+int hs_kv_pack(const void* pool, int L, int NB, int64_t page_bytes, const int64_t* block_ids,
+               int n, void* out, void* stream) {
+  if (n < 0 || L <= 0 || NB <= 0 || page_bytes <= 0)
+    return fail(HS_EINVAL, "pack sizes must be positive");
+  if (n == 0) return HS_OK;
+  if (!pool || !block_ids || !out) return fail(HS_EINVAL, "null pointer");
+  return launch_page_copy(pool, out, false, L, NB, page_bytes, block_ids, n,
+                          static_cast<hipStream_t>(stream));
+}
+
+int hs_kv_unpack(void* pool, int L, int NB, int64_t page_bytes, const int64_t* block_ids, int n,
+                 const void* in, void* stream) {
+  if (n < 0 || L <= 0 || NB <= 0 || page_bytes <= 0)
+    return fail(HS_EINVAL, "unpack sizes must be positive");
+  if (n == 0) return HS_OK;
+  if (!pool || !block_ids || !in) return fail(HS_EINVAL, "null pointer");
+  return launch_page_copy(pool, const_cast<void*>(in), true, L, NB, page_bytes, block_ids, n,
+                          static_cast<hipStream_t>(stream));
+}
+
+int hs_kv_gather(const void* cache, int NB, int BS, int64_t row_bytes, const int32_t* block_tables,
+                 int MB, int B, int length, void* out, void* stream) {
+  if (B < 0 || length < 0 || NB <= 0 || BS <= 0 || MB <= 0 || row_bytes <= 0)
+    return fail(HS_EINVAL, "gather sizes must be positive");
+  if ((int64_t)length > (int64_t)MB * BS)
+    return fail(HS_EINVAL, "length exceeds the block table's capacity");
+  if (B == 0 || length == 0) return HS_OK;
+  if (!cache || !block_tables || !out) return fail(HS_EINVAL, "null pointer");
+  return launch_gather_rows(cache, NB, BS, row_bytes, block_tables, MB, B, length, out,
+                            static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"

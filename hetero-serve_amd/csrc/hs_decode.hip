@@ -1,0 +1,310 @@
+// Paged attention over "rows": one query vector per (row, head) attending to
+// a prefix [0, end) of its sequence's paged KV.  Decode is B rows with
+// end = ctx_b; the VALU prefill path is B*S rows with end = ctx_b - S + s + 1.
+//
+// Algorithm (reference: paged_attn_v2.py:75-157 for the single pass,
+// paged_attn_v3.py:75-208 for split + merge): an online softmax over the
+// row's keys, optionally cut into partitions whose un-normalised states
+// (m, l, acc) are combined by a log-sum-exp merge.  The softmax runs in base 2
+// with scale * log2(e) folded into q, so every exponential is one v_exp_f32.
+//
+// Wave layout (gfx950, wave64).  A 16-byte load holds kVec KV elements, so one
+// token's head row of D elements is spread over kLpt = D / kVec lanes, and one
+// wave-wide load instruction covers kTpl = 64 / kLpt tokens.  For bf16 at
+// D = 128 that is 16 lanes per token and 4 tokens per load: a token's dot
+// product is reduced inside one 16-lane DPP row, with no LDS traffic.  Each
+// group of kLpt lanes ("slot") runs its own online softmax over the tokens it
+// loads; the kTpl slot states are merged once at the end of the partition.
+// A workgroup is 4 waves = 4 consecutive heads of the same (row, partition),
+// so the four waves stream adjacent 2*D-byte pieces of the same token rows.
+#include "hs_kernels.h"
+
+namespace hs {
+
+// Sequence of a row and the end of its key range (exclusive).  Returns false
+// for grid rows past the last real row (ragged batches size the grid by the
+// longest sequence).
+__device__ inline bool row_geometry(const RowAttnArgs& a, int row, int& b, int& end) {
+  int s, rows_b;
+  if (a.cu_q) {
+    if (row >= a.cu_q[a.B]) return false;
+    int lo = 0, hi = a.B;  // find b with cu_q[b] <= row < cu_q[b+1]
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (a.cu_q[mid] <= row) lo = mid; else hi = mid;
+    }
+    b = lo;
+    s = row - a.cu_q[b];
+    rows_b = a.cu_q[b + 1] - a.cu_q[b];
+  } else {
+    b = row / a.S;
+    s = row - b * a.S;
+    rows_b = a.S;
+  }
+  const int64_t cap = (int64_t)a.MB * a.BS;
+  const int64_t e = (int64_t)a.ctx[b] - rows_b + s + 1;
+  end = (int)(e < cap ? e : cap);
+  return true;
+}
+
+// Key range [lo, hi) of partition p; returns false when it is empty.
+__device__ inline bool partition_range(const RowAttnArgs& a, int end, int p, int& lo, int& hi,
+                                       int& nparts) {
+  if (end <= 0) {
+    nparts = 0;
+    return false;
+  }
+  int chunk;
+  if (a.mode == 0) chunk = end;
+  else if (a.mode == 1) chunk = a.part_tokens;
+  else chunk = (end + a.splits - 1) / a.splits;
+  nparts = (end + chunk - 1) / chunk;
+  lo = p * chunk;
+  hi = min(lo + chunk, end);
+  return p < nparts;
+}
+
+template <typename T, int D, bool kPaged>
+__global__ __launch_bounds__(256) void row_attn_part_kernel(RowAttnArgs a) {
+  constexpr int kVec = Elem<T>::kVec;
+  constexpr int kLpt = D / kVec;           // lanes per token
+  constexpr int kTpl = 64 / kLpt;          // tokens per wave-wide load
+  constexpr int kU = kTpl >= 16 ? 1 : 16 / kTpl;  // loads in flight per operand
+  constexpr int kStep = kTpl * kU;         // tokens per loop iteration
+  static_assert(kLpt >= 1 && kLpt <= 64 && 64 % kLpt == 0, "head_dim / lane split");
+
+  const int lane = threadIdx.x & 63;
+  const int h = blockIdx.y * 4 + (threadIdx.x >> 6);
+  if (h >= a.H) return;
+  const int row = blockIdx.x / a.P;
+  const int p = blockIdx.x - row * a.P;
+
+  int b, end;
+  if (!row_geometry(a, row, b, end)) return;
+  int lo = 0, hi = 0, nparts = 0;
+  const bool live = partition_range(a, end, p, lo, hi, nparts);
+  const int64_t orow = ((int64_t)row * a.H + h) * D;
+  if (!live) {
+    if (end <= 0 && p == 0) {  // nothing to attend to: a zero row
+      for (int d = lane; d < D; d += 64) a.out[orow + d] = 0.0f;
+    }
+    return;
+  }
+
+  const int r = lane / kLpt;  // token slot
+  const int c = lane % kLpt;  // element chunk
+  const int kvh = h / (a.H / a.Hkv);
+  const int64_t tok_stride = (int64_t)a.Hkv * D;
+  const int64_t blk_stride = tok_stride * a.BS;
+  const T* kp = reinterpret_cast<const T*>(a.k) + kvh * D + c * kVec;
+  const T* vp = reinterpret_cast<const T*>(a.v) + kvh * D + c * kVec;
+  const int32_t* bt = a.bt + (int64_t)b * a.MB;
+
+  float qv[kVec];
+  {
+    const float4* q4 = reinterpret_cast<const float4*>(a.q + orow + c * kVec);
+#pragma unroll
+    for (int i = 0; i < kVec / 4; ++i) {
+      const float4 x = q4[i];
+      qv[4 * i + 0] = x.x * a.qscale;
+      qv[4 * i + 1] = x.y * a.qscale;
+      qv[4 * i + 2] = x.z * a.qscale;
+      qv[4 * i + 3] = x.w * a.qscale;
+    }
+  }
+
+  float m = kNegBig, l = 0.0f;
+  float acc[kVec];
+#pragma unroll
+  for (int e = 0; e < kVec; ++e) acc[e] = 0.0f;
+
+  // Groups of kTpl tokens start at multiples of kTpl, so with kPaged
+  // (BS % kTpl == 0) a group never straddles a page and its block id is
+  // wave-uniform.  Addresses of groups past the range are clamped to the last
+  // group that holds a live token; their scores are masked below.
+  const int t_begin = lo - (lo % kTpl);
+  const int last_group = (hi - 1) - ((hi - 1) % kTpl);
+
+  for (int t0 = t_begin; t0 < hi; t0 += kStep) {
+    uint4 kr[kU], vr[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int tg = min(t0 + u * kTpl, last_group);
+      int64_t off;
+      if constexpr (kPaged) {
+        off = safe_block(bt[tg / a.BS], a.NB) * blk_stride +
+              (int64_t)(tg % a.BS + r) * tok_stride;
+      } else {
+        const int t = min(tg + r, hi - 1);
+        off = safe_block(bt[t / a.BS], a.NB) * blk_stride + (int64_t)(t % a.BS) * tok_stride;
+      }
+      kr[u] = load16(kp + off);
+      vr[u] = load16(vp + off);
+    }
+
+    float sc[kU];
+    bool ok[kU];
+    float mx = kNegBig;
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      float kf[kVec];
+      Elem<T>::to_f32(kr[u], kf);
+      float d = 0.0f;
+#pragma unroll
+      for (int e = 0; e < kVec; ++e) d = fmaf(qv[e], kf[e], d);
+      d = group_sum<kLpt>(d);
+      const int t = t0 + u * kTpl + r;
+      ok[u] = (t >= lo) && (t < hi);
+      sc[u] = ok[u] ? d : kNegBig;
+      mx = fmaxf(mx, sc[u]);
+    }
+    const float m_new = fmaxf(m, mx);
+    const float corr = fast_exp2(m - m_new);
+    float pu[kU];
+    float psum = 0.0f;
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      pu[u] = ok[u] ? fast_exp2(sc[u] - m_new) : 0.0f;
+      psum += pu[u];
+    }
+    l = fmaf(l, corr, psum);
+#pragma unroll
+    for (int e = 0; e < kVec; ++e) acc[e] *= corr;
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      float vf[kVec];
+      Elem<T>::to_f32(vr[u], vf);
+#pragma unroll
+      for (int e = 0; e < kVec; ++e) acc[e] = fmaf(pu[u], vf[e], acc[e]);
+    }
+    m = m_new;
+  }
+
+  // Merge the kTpl slot states: lanes with the same chunk c, different slot.
+#pragma unroll
+  for (int off = kLpt; off < 64; off <<= 1) {
+    const float m_o = __shfl_xor(m, off);
+    const float l_o = __shfl_xor(l, off);
+    const float mm = fmaxf(m, m_o);
+    const float w_s = fast_exp2(m - mm);
+    const float w_o = fast_exp2(m_o - mm);
+    l = l * w_s + l_o * w_o;
+#pragma unroll
+    for (int e = 0; e < kVec; ++e) acc[e] = acc[e] * w_s + __shfl_xor(acc[e], off) * w_o;
+    m = mm;
+  }
+
+  if (r != 0) return;
+  if (nparts == 1) {
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    float4* o4 = reinterpret_cast<float4*>(a.out + orow + c * kVec);
+#pragma unroll
+    for (int i = 0; i < kVec / 4; ++i)
+      o4[i] = make_float4(acc[4 * i] * inv, acc[4 * i + 1] * inv, acc[4 * i + 2] * inv,
+                          acc[4 * i + 3] * inv);
+  } else {
+    const int64_t pi = ((int64_t)row * a.H + h) * a.P + p;
+    float4* o4 = reinterpret_cast<float4*>(a.part_acc + pi * D + c * kVec);
+#pragma unroll
+    for (int i = 0; i < kVec / 4; ++i)
+      o4[i] = make_float4(acc[4 * i], acc[4 * i + 1], acc[4 * i + 2], acc[4 * i + 3]);
+    if (c == 0) *reinterpret_cast<float2*>(a.part_ml + 2 * pi) = make_float2(m, l);
+  }
+}
+
+// Log-sum-exp merge of the partition states of every (row, head) that has
+// more than one non-empty partition (reference: merge_splits_kernel,
+// paged_attn_v3.py:170-208).  One wave per (row, head), lanes over D.
+template <int D>
+__global__ __launch_bounds__(256) void row_attn_merge_kernel(RowAttnArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t w = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (w >= (int64_t)a.rows * a.H) return;
+  const int row = (int)(w / a.H);
+  int b, end;
+  if (!row_geometry(a, row, b, end)) return;
+  int lo, hi, nparts;
+  partition_range(a, end, 0, lo, hi, nparts);
+  if (nparts <= 1) return;  // written directly by the partition kernel
+
+  const float* ml = a.part_ml + w * a.P * 2;
+  float mm = kNegBig;
+  for (int p = 0; p < nparts; ++p) mm = fmaxf(mm, ml[2 * p]);
+
+  constexpr int kPer = (D + 63) / 64;
+  float acc[kPer];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) acc[i] = 0.0f;
+  float lsum = 0.0f;
+  for (int p = 0; p < nparts; ++p) {
+    const float wt = fast_exp2(ml[2 * p] - mm);
+    lsum = fmaf(ml[2 * p + 1], wt, lsum);
+    const float* pa = a.part_acc + (w * a.P + p) * D;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int d = lane + 64 * i;
+      if (d < D) acc[i] = fmaf(pa[d], wt, acc[i]);
+    }
+  }
+  const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int d = lane + 64 * i;
+    if (d < D) a.out[w * D + d] = acc[i] * inv;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// host launch
+// ---------------------------------------------------------------------------
+
+static int elem_vec(int kv_dtype) { return kv_dtype == HS_DTYPE_F32 ? 4 : 8; }
+
+// Tokens one wave-wide load covers for this dtype and head_dim.
+int row_attn_tokens_per_load(int kv_dtype, int D) { return 64 / (D / elem_vec(kv_dtype)); }
+
+template <typename T, int D>
+static void launch_typed(const RowAttnArgs& a, dim3 grid, hipStream_t stream) {
+  const int tpl = 64 / (D / Elem<T>::kVec);
+  profile_begin(stream);
+  if (a.BS % tpl == 0)
+    hipLaunchKernelGGL((row_attn_part_kernel<T, D, true>), grid, dim3(256), 0, stream, a);
+  else
+    hipLaunchKernelGGL((row_attn_part_kernel<T, D, false>), grid, dim3(256), 0, stream, a);
+  profile_end(stream);
+  if (a.P > 1) {
+    const int64_t waves = (int64_t)a.rows * a.H;
+    hipLaunchKernelGGL((row_attn_merge_kernel<D>), dim3((unsigned)((waves + 3) / 4)), dim3(256),
+                       0, stream, a);
+  }
+}
+
+template <typename T>
+static int launch_dim(const RowAttnArgs& a, int D, dim3 grid, hipStream_t stream) {
+  switch (D) {
+    case 32: launch_typed<T, 32>(a, grid, stream); break;
+    case 64: launch_typed<T, 64>(a, grid, stream); break;
+    case 128: launch_typed<T, 128>(a, grid, stream); break;
+    case 256: launch_typed<T, 256>(a, grid, stream); break;
+    default: return fail(HS_EUNSUPPORTED, "unsupported head_dim " + std::to_string(D));
+  }
+  return check_launch("paged attention");
+}
+
+// Launch the partition kernel (+ merge when P > 1).  Arguments are validated
+// by the caller.
+int launch_row_attn(const RowAttnArgs& a, int kv_dtype, int D, hipStream_t stream) {
+  const int64_t gx = (int64_t)a.rows * a.P;
+  if (gx <= 0) return HS_OK;
+  if (gx > 0x7fffffffLL)
+    return fail(HS_EUNSUPPORTED, "grid too large: rows * partitions = " + std::to_string(gx));
+  const dim3 grid((unsigned)gx, (unsigned)((a.H + 3) / 4));
+  switch (kv_dtype) {
+    case HS_DTYPE_F32: return launch_dim<float>(a, D, grid, stream);
+    case HS_DTYPE_F16: return launch_dim<_Float16>(a, D, grid, stream);
+    case HS_DTYPE_BF16: return launch_dim<Bf16>(a, D, grid, stream);
+    default: return fail(HS_EINVAL, "unknown kv dtype code " + std::to_string(kv_dtype));
+  }
+}
+
+}  // namespace hs

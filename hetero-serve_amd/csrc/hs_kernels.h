@@ -1,0 +1,51 @@
+// Internal interface between the C-ABI layer (hs_api.hip) and the kernel
+// translation units.
+#pragma once
+
+#include "hs_common.h"
+
+namespace hs {
+
+// Paged attention over rows: one query vector per (row, head).  Filled by
+// hs_api.hip, consumed by the kernels in hs_decode.hip.
+struct RowAttnArgs {
+  const float* q;         // [rows, H, D]
+  const void* k;          // [NB, BS, Hkv, D]
+  const void* v;
+  const int32_t* bt;      // [B, MB]
+  const int32_t* ctx;     // [B]
+  const int32_t* cu_q;    // [B + 1] row offsets, or null for S rows per sequence
+  float* out;             // [rows, H, D]
+  float* part_acc;        // [rows, H, P, D]   un-normalised partial outputs
+  float* part_ml;         // [rows, H, P, 2]   partial (max, sum), base-2 domain
+  int rows;               // rows in the grid (>= real rows when cu_q is set)
+  int S;                  // rows per sequence when cu_q is null
+  int B, H, Hkv, BS, MB, NB;
+  int mode;               // 0 one pass, 1 fixed partitions, 2 num_splits slices
+  int part_tokens;        // mode 1
+  int splits;             // mode 2
+  int P;                  // partition slots per (row, head) in the grid
+  float qscale;           // scale * log2(e)
+};
+
+// Measurement hook of hs_profile_next_launch: bracket the main kernel of the
+// current call with the caller's events (no-ops when none are pending).
+void profile_begin(hipStream_t stream);
+void profile_end(hipStream_t stream);
+
+int launch_row_attn(const RowAttnArgs& a, int kv_dtype, int D, hipStream_t stream);
+
+int launch_page_copy(const void* pool, void* buf, bool unpack, int L, int NB, int64_t page_bytes,
+                     const int64_t* ids, int n, hipStream_t stream);
+
+int launch_gather_rows(const void* cache, int NB, int BS, int64_t row_bytes, const int32_t* bt,
+                       int MB, int B, int length, void* out, hipStream_t stream);
+
+// Matrix-core causal prefill (hs_prefill_mfma.hip).  cu_q null: S rows per
+// sequence, q/out [B, S, H, D]; else ragged rows as in hs_prefill_varlen.
+int launch_prefill_mfma(const float* q, const int32_t* cu_q, int S, int max_rows_per_seq,
+                        const void* k, const void* v, int kv_dtype, int NB, const int32_t* bt,
+                        const int32_t* ctx, float* out, int B, int H, int Hkv, int D, int BS,
+                        int MB, float scale, hipStream_t stream);
+
+}  // namespace hs

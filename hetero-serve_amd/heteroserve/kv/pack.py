@@ -1,0 +1,165 @@
+"""KV-block migration pack/unpack and contiguous gather on the GPU.
+
+The pool is hetero-serve's device KV tensor ``[L, 2, num_blocks, block_size,
+n_kv_heads, head_dim]`` (heteroserve/kv/torch_blocks.py:48, layout from
+heteroserve/kv/blocks.py:72-81).  A migration payload is
+``[n, L, 2, block_size, n_kv_heads, head_dim]`` in the pool dtype, the wire
+format both of the reference's transports carry.
+
+    export_blocks_device  pool -> payload   torch_blocks.py:137-148
+    write_blocks_device   payload -> pool   torch_blocks.py:150-154
+    gather_kv_batch       pool layer -> [B, length, Hkv, D]   torch_blocks.py:125-135
+
+Each is one libhsattn launch (a bitwise page copy) instead of the reference's
+advanced-index gather plus permute-copy, or its Python loop of one copy per
+block.  Block ids follow torch indexing rules: negative ids count from the
+end of the pool, and an id outside [-num_blocks, num_blocks) raises
+IndexError before anything is launched.
+
+``HipKVMixin`` carries these as methods, so the reference allocator picks them
+up by inheritance:
+
+    class TorchBlockAllocator(HipKVMixin, _ReferenceTorchBlockAllocator): ...
+"""
+
+from __future__ import annotations
+
+from typing import Sequence
+
+from .. import _hip
+
+
+def _normalise_ids(block_ids, num_blocks: int) -> list[int]:
+    """Block ids as Python ints, negatives wrapped as torch indexing does."""
+    import torch
+
+    if torch.is_tensor(block_ids):
+        block_ids = block_ids.detach().to("cpu").reshape(-1).tolist()
+    out = []
+    for raw in block_ids:
+        i = int(raw)
+        if not -num_blocks <= i < num_blocks:
+            raise IndexError(
+                f"index {i} is out of bounds for dimension 2 with size {num_blocks}")
+        out.append(i + num_blocks if i < 0 else i)
+    return out
+
+
+def _ids_tensor(ids: Sequence[int], device):
+    import torch
+
+    return torch.as_tensor(ids, dtype=torch.int64).to(device, non_blocking=False)
+
+
+def _check_pool(pool) -> None:
+    if pool.dim() != 6 or pool.shape[1] != 2:
+        raise RuntimeError("pool must be [L, 2, num_blocks, block_size, n_kv_heads, head_dim]")
+    if not pool.is_contiguous():
+        raise RuntimeError("pool must be contiguous")
+    if not pool.is_cuda:
+        raise RuntimeError("pool must be on CUDA")
+
+
+def export_blocks_device(pool, block_ids):
+    """pool[:, :, ids].permute(2, 0, 1, 3, 4, 5).contiguous(), bit for bit."""
+    import torch
+
+    _hip.lib("KV pack HIP kernel")
+    _check_pool(pool)
+    ids = _normalise_ids(block_ids, pool.shape[2])
+    L, _, _, BS, H, D = pool.shape
+    out = torch.empty((len(ids), L, 2, BS, H, D), dtype=pool.dtype, device=pool.device)
+    if ids:
+        _hip.kv_pack(pool, _ids_tensor(ids, pool.device), out)
+    return out
+
+
+def write_blocks_device(pool, block_ids, payload) -> None:
+    """pool[:, :, block_ids[i]] = payload[i] for every i, in one launch.
+
+    The payload is converted to the pool's device and dtype first, as the
+    reference's ``payload.to(device, dtype)`` does.  When an id repeats, the
+    last payload entry for it wins, which is what the reference's sequential
+    loop leaves behind.
+    """
+    _hip.lib("KV unpack HIP kernel")
+    _check_pool(pool)
+    ids = _normalise_ids(block_ids, pool.shape[2])
+    if not ids:
+        return
+    data = payload.to(device=pool.device, dtype=pool.dtype)
+    block_shape = tuple(pool.shape[:2]) + tuple(pool.shape[3:])
+    if data.dim() != 6 or tuple(data.shape[1:]) != block_shape or data.shape[0] < len(ids):
+        raise RuntimeError(
+            f"payload must be [n >= {len(ids)}, {', '.join(map(str, block_shape))}], "
+            f"got {list(data.shape)}")
+    last = {blk: i for i, blk in enumerate(ids)}
+    if len(last) != len(ids):  # duplicates: keep each block's final write
+        order = sorted(last.items(), key=lambda kv: kv[1])
+        ids = [blk for blk, _ in order]
+        data = data[[i for _, i in order]]
+    data = data[: len(ids)].contiguous()
+    _hip.kv_unpack(pool, _ids_tensor(ids, pool.device), data)
+
+
+def gather_kv_batch(pool, tables, length: int, layer: int):
+    """([B, length, Hkv, D], same for V): each sequence's first `length` tokens.
+
+    tables is a list of per-sequence block-id lists, as the reference takes;
+    every list must cover `length` tokens.
+    """
+    import torch
+
+    _hip.lib("KV gather HIP kernel")
+    _check_pool(pool)
+    L, _, NB, BS, H, D = pool.shape
+    if not 0 <= layer < L:
+        raise IndexError(f"layer {layer} out of range for {L} layers")
+    need = -(-int(length) // BS)
+    rows = []
+    for t in tables:
+        ids = _normalise_ids(list(t)[:need], NB)
+        if len(ids) < need:
+            raise IndexError(
+                f"block table of {len(ids)} blocks cannot hold {length} tokens")
+        rows.append(ids)
+    B = len(rows)
+    k_out = torch.empty((B, length, H, D), dtype=pool.dtype, device=pool.device)
+    v_out = torch.empty_like(k_out)
+    if B == 0 or length == 0:
+        return k_out, v_out
+    bt = torch.as_tensor(rows, dtype=torch.int32).reshape(B, need).to(pool.device)
+    _hip.kv_gather(pool[layer, 0], bt, length, k_out)
+    _hip.kv_gather(pool[layer, 1], bt, length, v_out)
+    return k_out, v_out
+
+
+class HipKVMixin:
+    """GPU storage methods for hetero-serve's TorchBlockAllocator.
+
+    Expects ``self.pool`` (the device pool), ``self.device`` and
+    ``self.torch_dtype`` as TorchBlockAllocator defines them
+    (torch_blocks.py:33-48).  Overrides the methods of torch_blocks.py:125-175
+    that move KV pages.
+    """
+
+    def export_blocks_device(self, block_ids):
+        return export_blocks_device(self.pool, block_ids)
+
+    def write_blocks_device(self, block_ids, payload) -> None:
+        write_blocks_device(self.pool, block_ids, payload)
+
+    def export_blocks(self, block_ids):
+        """Host copy of the payload (numpy), for the shaped-TCP transport."""
+        return export_blocks_device(self.pool, block_ids).cpu().numpy()
+
+    def write_blocks(self, block_ids, payload) -> None:
+        import numpy as np
+        import torch
+
+        data = torch.as_tensor(np.ascontiguousarray(payload), dtype=self.torch_dtype,
+                               device=self.device)
+        write_blocks_device(self.pool, block_ids, data)
+
+    def gather_kv_batch(self, tables, length: int, layer: int):
+        return gather_kv_batch(self.pool, tables, length, layer)

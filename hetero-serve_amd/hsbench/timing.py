@@ -1,0 +1,84 @@
+"""HIP-event timing for the benchmark, through the HIP runtime directly.
+
+Events are created with hipEventCreate and recorded either here (around a
+whole timed region, on torch's current stream) or by libhsattn itself
+(hs_profile_next_launch brackets one kernel on the stream it launches on).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import ctypes.util
+from typing import Callable, List, Tuple
+
+_hip = None
+
+
+def _rt():
+    global _hip
+    if _hip is None:
+        name = ctypes.util.find_library("amdhip64") or "libamdhip64.so"
+        _hip = ctypes.CDLL(name)
+        _hip.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        _hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        _hip.hipEventSynchronize.argtypes = [ctypes.c_void_p]
+        _hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p,
+                                             ctypes.c_void_p]
+        _hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
+    return _hip
+
+
+def _ok(rc: int, what: str) -> None:
+    if rc != 0:
+        raise RuntimeError(f"{what} failed with HIP error {rc}")
+
+
+class Event:
+    def __init__(self):
+        self.handle = ctypes.c_void_p()
+        _ok(_rt().hipEventCreate(ctypes.byref(self.handle)), "hipEventCreate")
+
+    def record(self, stream: int) -> None:
+        _ok(_rt().hipEventRecord(self.handle, ctypes.c_void_p(stream)), "hipEventRecord")
+
+    def elapsed_ms(self, end: "Event") -> float:
+        _ok(_rt().hipEventSynchronize(end.handle), "hipEventSynchronize")
+        ms = ctypes.c_float()
+        _ok(_rt().hipEventElapsedTime(ctypes.byref(ms), self.handle, end.handle),
+            "hipEventElapsedTime")
+        return float(ms.value)
+
+    def __del__(self):
+        if _hip is not None and self.handle:
+            _hip.hipEventDestroy(self.handle)
+
+
+def time_steps(step: Callable[[], None], steps: int, warmup: int, stream: int,
+               arm: Callable[[Event, Event], None]) -> Tuple[float, List[float], float]:
+    """Run `warmup` untimed steps, then `steps` timed ones.
+
+    `arm(start, stop)` is called before each timed step to ask libhsattn to
+    bracket that step's main kernel.  Returns (mean step ms over the region,
+    per-step kernel ms, host wall seconds of the region).
+    """
+    import time
+
+    import torch
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    pairs = [(Event(), Event()) for _ in range(steps)]
+    region0, region1 = Event(), Event()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    region0.record(stream)
+    for s, e in pairs:
+        arm(s, e)
+        step()
+    region1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    step_ms = region0.elapsed_ms(region1) / max(steps, 1)
+    kernel_ms = [s.elapsed_ms(e) for s, e in pairs]
+    return step_ms, kernel_ms, wall

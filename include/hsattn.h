@@ -1,0 +1,201 @@
+/*
+ * hsattn.h -- C ABI of the MI355X (gfx950) paged-attention library libhsattn.so.
+ *
+ * This is the drop-in boundary for hetero-serve's paged-attention hot path.
+ * Each entry point replaces one pybind function that the reference builds
+ * with torch.utils.cpp_extension.load_inline from CUDA source embedded in a
+ * Python string; the citation above each declaration names that function
+ * (paths relative to the reference checkout).  Nothing here uses torch or
+ * pybind types: tensors cross as plain device pointers plus sizes, and the
+ * stream crosses as an opaque hipStream_t handle (void*).
+ *
+ * Conventions shared by every entry point
+ *   - All pointers are device pointers on the current HIP device, except
+ *     where a comment says otherwise.
+ *   - Every launch goes on `stream` (NULL = the null stream). Nothing here
+ *     synchronises the stream, allocates memory or keeps state between
+ *     calls, so calls are re-entrant and may run on several host threads.
+ *   - Return value: HS_OK (0) on success, a negative HS_E* code otherwise.
+ *     The message for the last failure on the calling thread is returned by
+ *     hs_last_error().
+ *   - KV pages are token-major, as the reference allocator lays them out
+ *     (heteroserve/kv/blocks.py:72-81): a cache is [num_blocks, block_size,
+ *     n_kv_heads, head_dim] with the inner three dimensions contiguous.
+ *   - Block tables are [B, max_blocks] int32, padded with -1; a position j of
+ *     sequence b lives in block block_tables[b][j / block_size] at offset
+ *     j % block_size (heteroserve/model/paged_attn_v2.py:124-127).  Entries
+ *     outside [0, num_blocks) are read as block 0 (the torch reference clamps
+ *     negatives to 0, paged_attn.py:275), so a bad table can never make a
+ *     kernel read outside the pool.
+ */
+#ifndef HSATTN_H
+#define HSATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HS_ABI_VERSION 1
+
+/* KV element type codes (the pool dtype). */
+#define HS_DTYPE_F32 0
+#define HS_DTYPE_F16 1
+#define HS_DTYPE_BF16 2
+
+/* Status codes. */
+#define HS_OK 0
+#define HS_EINVAL (-1)       /* bad argument: shape, pointer, size         */
+#define HS_EUNSUPPORTED (-2) /* geometry this library does not serve       */
+#define HS_EHIP (-3)         /* the HIP runtime reported an error          */
+#define HS_EWORKSPACE (-4)   /* workspace missing or too small             */
+
+/* ABI version of the loaded library; the Python loader refuses a mismatch. */
+int hs_abi_version(void);
+
+/* Message of the last failed call on this thread ("" when none).  Valid
+ * until the next call into the library from the same thread. */
+const char* hs_last_error(void);
+
+/*
+ * Measurement hook (no reference counterpart).  The next libhsattn call made
+ * from this thread records `start_event` on its stream just before its main
+ * kernel (the partition kernel of hs_decode, the attention kernel of
+ * hs_prefill*, the copy kernel of hs_kv_*) and `stop_event` just after it, so
+ * a benchmark can time that one kernel on the stream it runs on.  The events
+ * are hipEvent_t handles owned by the caller; one call consumes them.
+ * Passing NULL, NULL cancels a pending request.
+ */
+int hs_profile_next_launch(void* start_event, void* stop_event);
+
+/* Compute units of HIP device `device` (256 on MI355X); -1 on error. */
+int hs_device_cu_count(int device);
+
+/*
+ * Split count heuristic of the v3 decode path.
+ * Replaces: choose_num_splits, heteroserve/model/paged_attn_v3.py:212-232.
+ *   clamp(max(max_context / 32, ceil(CUs * 8 / (num_seqs * num_heads))), 1, 64)
+ * with CUs taken from the current HIP device.  Returns -1 on error.
+ */
+int64_t hs_choose_num_splits(int64_t num_seqs, int64_t num_heads, int64_t max_context);
+
+/*
+ * Workspace bytes hs_decode needs for these sizes (0 when it needs none).
+ * num_splits and partition_tokens as for hs_decode.
+ */
+size_t hs_decode_workspace_bytes(int B, int H, int D, int BS, int MB, int num_splits,
+                                 int partition_tokens);
+
+/*
+ * Decode attention, one query token per sequence:
+ *   out[b,h,:] = softmax(scale * q[b,h,:] . K[b,j,kvh,:] over j < ctx_b) . V[b,j,kvh,:]
+ * with kvh = h / (H / Hkv) and ctx_b = min(context_lens[b], MB * BS).
+ * A sequence with ctx_b <= 0 gets a zero output row.
+ *
+ * Replaces three reference entry points, which compute the same function:
+ *   paged_attention     heteroserve/model/paged_attn.py:136-183     (v1)
+ *   paged_attention_v2  heteroserve/model/paged_attn_v2.py:159-212  (v2)
+ *   paged_attention_v3  heteroserve/model/paged_attn_v3.py:234-303  (v3)
+ *
+ *   q            [B, H, D] float32
+ *   k_cache      [num_blocks, BS, Hkv, D] of kv_dtype (same for v_cache)
+ *   block_tables [B, MB] int32;  context_lens [B] int32
+ *   out          [B, H, D] float32
+ *   D            32, 64, 128 or 256;  H % Hkv == 0
+ *   num_splits   1  = one pass per (sequence, head)               (v2)
+ *                >1 = the context cut into num_splits slices of
+ *                     ceil(ctx_b / num_splits) tokens, then an
+ *                     log-sum-exp merge                            (v3)
+ *                0  = fixed partitions of partition_tokens tokens
+ *                     plus the merge (the fast default)
+ *   partition_tokens  used when num_splits == 0; 0 = library default.
+ *                Must be a multiple of 16.
+ *   workspace    device scratch of hs_decode_workspace_bytes(...) bytes
+ *                (may be NULL when that is 0).
+ */
+int hs_decode(const float* q, const void* k_cache, const void* v_cache, int kv_dtype,
+              int num_blocks, const int32_t* block_tables, const int32_t* context_lens,
+              float* out, int B, int H, int Hkv, int D, int BS, int MB, float scale,
+              int num_splits, int partition_tokens, void* workspace,
+              size_t workspace_bytes, void* stream);
+
+/*
+ * Causal chunked prefill over the paged cache.  Query s of sequence b sits at
+ * absolute position ctx_b - S + s and attends to keys [0, ctx_b - S + s]; rows
+ * whose position is negative (padding in front of a short sequence) are zero.
+ * The chunk's own K/V must already be in the pool.
+ *
+ * Replaces:
+ *   use_mfma = 0: paged_attention_prefill,
+ *                 heteroserve/model/paged_attn_prefill.py:159-214
+ *                 (fp32 VALU arithmetic, any KV dtype, D in {32,64,128,256})
+ *   use_mfma = 1: paged_attention_prefill_wmma,
+ *                 heteroserve/model/paged_attn_wmma.py:256-318
+ *                 (fp16 matrix-core operands with fp32 accumulation; KV dtype
+ *                 f16 or bf16, BS == 16, D in {32,64,128})
+ *
+ *   q   [B, S, H, D] float32;  out [B, S, H, D] float32
+ */
+int hs_prefill(const float* q, const void* k_cache, const void* v_cache, int kv_dtype,
+               int num_blocks, const int32_t* block_tables, const int32_t* context_lens,
+               float* out, int B, int S, int H, int Hkv, int D, int BS, int MB, float scale,
+               int use_mfma, void* stream);
+
+/*
+ * Ragged-batch form of hs_prefill (use_mfma as there): sequence b owns query
+ * rows [cu_seqlens_q[b], cu_seqlens_q[b+1]) of q [total, H, D] and out, with
+ * S_b = cu_seqlens_q[b+1] - cu_seqlens_q[b] <= max_seqlen_q.  Query i of
+ * sequence b sits at position ctx_b - S_b + i.  No reference counterpart: the
+ * reference's engine calls prefill with B = 1 per chunk
+ * (heteroserve/model/torch_engine.py:292-313), and this entry point runs
+ * several such chunks in one launch.
+ */
+int hs_prefill_varlen(const float* q, const int32_t* cu_seqlens_q, int max_seqlen_q,
+                      const void* k_cache, const void* v_cache, int kv_dtype, int num_blocks,
+                      const int32_t* block_tables, const int32_t* context_lens, float* out,
+                      int B, int H, int Hkv, int D, int BS, int MB, float scale,
+                      int use_mfma, void* stream);
+
+/*
+ * KV-block pack for migration:
+ *   out[i, l, c] = pool[l, c, block_ids[i]]      (c = 0 for K, 1 for V)
+ * where one page is page_bytes = BS * Hkv * D * itemsize bytes, pool is
+ * [L, 2, NB, page] and out is [n, L, 2, page].  A bitwise copy.
+ * Replaces: TorchBlockAllocator.export_blocks_device,
+ *           heteroserve/kv/torch_blocks.py:137-148
+ * (pool[:, :, idx].permute(2, 0, 1, 3, 4, 5).contiguous()).
+ * block_ids is a device int64 array; ids outside [0, NB) are skipped (the
+ * Python layer rejects them first, as torch indexing would).
+ */
+int hs_kv_pack(const void* pool, int L, int NB, int64_t page_bytes, const int64_t* block_ids,
+               int n, void* out, void* stream);
+
+/*
+ * Inverse of hs_kv_pack:  pool[l, c, block_ids[i]] = in[i, l, c].
+ * Replaces: TorchBlockAllocator.write_blocks_device,
+ *           heteroserve/kv/torch_blocks.py:150-154 (a Python loop of one
+ *           copy per block).  block_ids must not repeat.
+ */
+int hs_kv_unpack(void* pool, int L, int NB, int64_t page_bytes, const int64_t* block_ids,
+                 int n, const void* in, void* stream);
+
+/*
+ * Contiguous gather of the first `length` tokens of every sequence:
+ *   out[b, t] = cache[block_tables[b][t / BS], t % BS]
+ * for one layer's K (or V) cache [NB, BS, row] with row = row_bytes bytes
+ * (Hkv * D * itemsize); out is [B, length, row].
+ * Replaces: TorchBlockAllocator.gather_kv_batch,
+ *           heteroserve/kv/torch_blocks.py:125-135 (the per-layer gather
+ *           that the fused decode kernels make unnecessary).
+ */
+int hs_kv_gather(const void* cache, int NB, int BS, int64_t row_bytes,
+                 const int32_t* block_tables, int MB, int B, int length, void* out,
+                 void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HSATTN_H */

@@ -1,0 +1,148 @@
+"""CPU checks of the C-ABI boundary and the Python module state (no GPU needed).
+
+The library must load without a GPU, export every function include/hsattn.h
+declares, and reject bad arguments before touching the device.  The Python
+modules keep the reference's module-state API and never compute on the CPU.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "hsattn.h"
+
+
+def _declared_functions() -> list[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(hs_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from heteroserve import _hip
+
+    if not _hip.lib_path().exists():
+        pytest.fail(f"{_hip.lib_path()} missing: run python hetero-serve_amd/build.py")
+    return _hip.open_library()
+
+
+def test_header_declarations_are_bound_by_the_loader():
+    from heteroserve import _hip
+
+    assert _declared_functions() == sorted(_hip.EXPORTED_SYMBOLS)
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in _declared_functions():
+        assert hasattr(lib, name), name
+    assert lib.hs_abi_version() == 1
+    assert lib.hs_last_error() == b""
+
+
+def test_argument_errors_need_no_device(lib):
+    """Validation happens before any HIP call: these return codes and
+    messages come back on a machine without a GPU."""
+    fake = ctypes.c_void_p(0x1000)
+    rc = lib.hs_decode(None, None, None, 0, 8, None, None, None, 1, 4, 4, 64, 16, 2,
+                       0.1, 0, 0, None, 0, None)
+    assert rc == -1 and b"null" in lib.hs_last_error()
+    rc = lib.hs_decode(fake, fake, fake, 0, 8, fake, fake, fake, 1, 6, 4, 64, 16, 2,
+                       0.1, 0, 0, None, 0, None)
+    assert rc == -1 and b"divisible" in lib.hs_last_error()
+    rc = lib.hs_decode(fake, fake, fake, 0, 8, fake, fake, fake, 1, 4, 4, 96, 16, 2,
+                       0.1, 0, 0, None, 0, None)
+    assert rc == -2 and b"head_dim" in lib.hs_last_error()
+    rc = lib.hs_decode(fake, fake, fake, 5, 8, fake, fake, fake, 1, 4, 4, 64, 16, 2,
+                       0.1, 0, 0, None, 0, None)
+    assert rc == -1 and b"dtype" in lib.hs_last_error()
+    # partitioned decode needs a workspace
+    need = lib.hs_decode_workspace_bytes(2, 4, 64, 16, 64, 0, 0)
+    assert need > 0
+    rc = lib.hs_decode(fake, fake, fake, 1, 8, fake, fake, fake, 2, 4, 4, 64, 16, 64,
+                       0.1, 0, 0, None, 0, None)
+    assert rc == -4 and b"workspace" in lib.hs_last_error()
+    assert lib.hs_decode_workspace_bytes(2, 4, 64, 16, 64, 1, 0) == 0      # one pass
+    assert lib.hs_decode_workspace_bytes(2, 4, 64, 16, 64, 0, 24) == 0     # bad partition
+    rc = lib.hs_prefill(fake, fake, fake, 0, 8, fake, fake, fake, 1, 4, 4, 4, 64, 16, 2,
+                        0.1, 1, None)
+    assert rc == -2 and b"fp16 or bf16" in lib.hs_last_error()
+    rc = lib.hs_prefill(fake, fake, fake, 1, 8, fake, fake, fake, 1, 4, 4, 4, 64, 32, 2,
+                        0.1, 1, None)
+    assert rc == -2 and b"block_size == 16" in lib.hs_last_error()
+    rc = lib.hs_kv_pack(None, 1, 8, 1024, None, 3, None, None)
+    assert rc == -1
+    assert lib.hs_kv_pack(None, 1, 8, 1024, None, 0, None, None) == 0      # nothing to do
+    rc = lib.hs_kv_gather(fake, 8, 16, 512, fake, 2, 1, 33, fake, None)
+    assert rc == -1 and b"capacity" in lib.hs_last_error()
+    rc = lib.hs_profile_next_launch(fake, None)
+    assert rc == -1
+    assert lib.hs_profile_next_launch(None, None) == 0
+
+
+def test_workspace_size_formula(lib):
+    """hs_decode's workspace: (rows * H * P * D) floats, padded to 256 bytes,
+    then rows * H * P (max, sum) pairs; P = ceil(MB * BS / partition)."""
+    B, H, D, BS, MB = 3, 5, 128, 16, 100
+    for part, P in ((256, 7), (512, 4), (16, 100)):
+        acc = (B * H * P * D * 4 + 255) // 256 * 256
+        assert lib.hs_decode_workspace_bytes(B, H, D, BS, MB, 0, part) == acc + B * H * P * 8
+    acc = (B * H * 9 * D * 4 + 255) // 256 * 256
+    assert lib.hs_decode_workspace_bytes(B, H, D, BS, MB, 9, 0) == acc + B * H * 9 * 8
+
+
+def test_module_state_without_a_device(monkeypatch):
+    """On a host without a HIP device the modules report why, keep the
+    reference's availability API, and raise instead of computing."""
+    import torch
+
+    from heteroserve.model import (paged_attn, paged_attn_prefill, paged_attn_v2,
+                                   paged_attn_v3, paged_attn_wmma)
+
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    assert paged_attn.which_backend() == "torch"
+    assert "no HIP device" in paged_attn.build_error()
+    for m in (paged_attn_v2, paged_attn_v3, paged_attn_prefill, paged_attn_wmma):
+        assert m.is_available() is False
+        assert m.build_error()
+    q = torch.zeros(1, 4, 64)
+    k = torch.zeros(4, 16, 4, 64)
+    bt = torch.zeros(1, 1, dtype=torch.int32)
+    ctx = torch.ones(1, dtype=torch.int32)
+    with pytest.raises(RuntimeError, match="unavailable"):
+        paged_attn.paged_attention(q, k, k, bt, ctx, 0.1)
+    with pytest.raises(RuntimeError, match="unavailable"):
+        paged_attn_v2.paged_attention_v2(q, k, k, bt, ctx, 0.1)
+    with pytest.raises(RuntimeError, match="unavailable"):
+        paged_attn_v3.paged_attention_v3(q, k, k, bt, ctx, 0.1, 4)
+    with pytest.raises(RuntimeError, match="unavailable"):
+        paged_attn_prefill.paged_attention_prefill(q[:, None], k, k, bt, ctx, 0.1)
+    with pytest.raises(RuntimeError, match="unavailable"):
+        paged_attn_wmma.paged_attention_prefill_wmma(q[:, None], k, k, bt, ctx, 0.1)
+    # the reference's geometry gate (tests/test_torch_engine.py:642-653)
+    assert paged_attn_wmma.supports(32, 64, torch.float16) is False
+    assert paged_attn_wmma.supports(16, 64, torch.float32) is False
+    assert paged_attn_wmma.supports(16, 48, torch.float16) is False
+    assert paged_attn_v2.bytes_moved(16, 512, 12, 64, 2) == 25_165_824
+    assert paged_attn_v2.peak_bandwidth_gbs() is None
+
+
+def test_disable_flag_is_honoured(monkeypatch):
+    """HETEROSERVE_DISABLE_CUDA_KERNEL (reference paged_attn.py:208-210)."""
+    import importlib
+
+    from heteroserve import _hip
+
+    monkeypatch.setenv("HETEROSERVE_DISABLE_CUDA_KERNEL", "1")
+    fresh = importlib.reload(_hip)
+    try:
+        assert not fresh.ready()
+        assert "HETEROSERVE_DISABLE_CUDA_KERNEL" in fresh.error()
+    finally:
+        monkeypatch.delenv("HETEROSERVE_DISABLE_CUDA_KERNEL")
+        importlib.reload(_hip)

@@ -1,0 +1,308 @@
+"""GPU parity of the decode kernels (v1 / v2 / v3 entry points) against the oracle.
+
+Restates the reference's kernel gates (tests/test_torch_engine.py:199-218,
+:284-319, :405-470) on libhsattn, then adds the benchmark configurations and
+the edge cases the reference leaves implicit.  Every comparison is against
+the CPU oracle (oracle/attention.py) on the same inputs, copied back from the
+device; tolerances are written at each assertion.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+from _refcases import build_paged_case, lay_out, table_array  # noqa: E402
+from oracle.attention import decode_one, paged_attention_torch  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def _mods():
+    from heteroserve.model import paged_attn, paged_attn_v2, paged_attn_v3
+
+    assert paged_attn.which_backend() == "cuda", paged_attn.build_error()
+    return paged_attn, paged_attn_v2, paged_attn_v3
+
+
+def _ref_case(seed=5, lens=(9, 31, 16), dtype=torch.float32):
+    c = build_paged_case(seed=seed, lens=lens)
+    pool = torch.as_tensor(c["pool"]).to(DEV, dtype)
+    bt = torch.as_tensor(table_array(c["tables"])).to(DEV)
+    ctx = torch.tensor(c["lens"], dtype=torch.int32, device=DEV)
+    q = torch.as_tensor(c["q"], device=DEV)
+    return pool, bt, ctx, q, c["scale"]
+
+
+def _oracle(q, k, v, bt, ctx, scale):
+    return paged_attention_torch(q.cpu(), k.cpu(), v.cpu(), bt.cpu(), ctx.cpu(), scale)
+
+
+def _maxerr(a, b) -> float:
+    return (a.detach().float().cpu() - b.detach().float().cpu()).abs().max().item()
+
+
+# ---------------------------------------------------------------------------
+# the reference's kernel gates
+# ---------------------------------------------------------------------------
+
+
+def test_v1_matches_torch_reference():
+    """tests/test_torch_engine.py:199-218, tolerance 1e-3."""
+    m1, _, _ = _mods()
+    pool, bt, ctx, q, scale = _ref_case()
+    got = m1.paged_attention(q, pool[0, 0], pool[0, 1], bt, ctx, scale)
+    want = _oracle(q, pool[0, 0], pool[0, 1], bt, ctx, scale)
+    np.testing.assert_allclose(got.cpu().numpy(), want.numpy(), rtol=1e-3, atol=1e-3)
+
+
+def test_v2_matches_reference_and_v1():
+    """tests/test_torch_engine.py:284-319 (seeds 5 and 9), tolerance 1e-3."""
+    m1, m2, _ = _mods()
+    assert m2.is_available(), m2.build_error()
+    for seed in (5, 9):
+        pool, bt, ctx, q, scale = _ref_case(seed=seed)
+        a = m1.paged_attention(q, pool[0, 0], pool[0, 1], bt, ctx, scale)
+        b = m2.paged_attention_v2(q, pool[0, 0], pool[0, 1], bt, ctx, scale)
+        want = _oracle(q, pool[0, 0], pool[0, 1], bt, ctx, scale)
+        np.testing.assert_allclose(b.cpu().numpy(), want.numpy(), rtol=1e-3, atol=1e-3)
+        np.testing.assert_allclose(a.cpu().numpy(), b.cpu().numpy(), rtol=1e-3, atol=1e-3)
+
+
+def test_v3_every_split_count_matches_reference():
+    """tests/test_torch_engine.py:405-429: splits {0,1,2,4,8,16,64}, 1e-3."""
+    _, _, m3 = _mods()
+    pool, bt, ctx, q, scale = _ref_case()
+    want = _oracle(q, pool[0, 0], pool[0, 1], bt, ctx, scale).numpy()
+    for splits in (0, 1, 2, 4, 8, 16, 64):
+        got = m3.paged_attention_v3(q, pool[0, 0], pool[0, 1], bt, ctx, scale, splits)
+        np.testing.assert_allclose(got.cpu().numpy(), want, rtol=1e-3, atol=1e-3,
+                                   err_msg=f"num_splits={splits}")
+
+
+def test_choose_num_splits_uses_the_device_cu_count():
+    """paged_attn_v3.py:212-232 with the device's CU count."""
+    _, _, m3 = _mods()
+    from oracle.splits import choose_num_splits
+
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    for args in [(16, 12, 512), (32, 12, 2048), (1, 1, 16), (64, 32, 8192), (2, 2, 40)]:
+        assert m3.choose_num_splits(*args) == choose_num_splits(*args, cus), args
+
+
+def test_all_three_entry_points_agree_under_fuzz():
+    """tests/test_torch_engine.py:432-470: 15 trials, fp16 KV, BS in {8,16,32}, err < 5e-3."""
+    m1, m2, m3 = _mods()
+    rng = np.random.default_rng(7)
+    gen = torch.Generator(device=DEV).manual_seed(7)
+    for trial in range(15):
+        n_seqs = int(rng.integers(1, 9))
+        bs = int(rng.choice([8, 16, 32]))
+        lens = [int(rng.integers(1, 700)) for _ in range(n_seqs)]
+        need = sum(-(-n // bs) for n in lens) + 8
+        seqs = []
+        for n in lens:
+            rng.integers(1, 4000, size=n)
+            k = rng.standard_normal((4, 4, n, 64)).astype(np.float16)
+            seqs.append((k, k))
+        pool_np, tables = lay_out(seqs, bs, max(32, need), 4, np.float16)
+        pool = torch.as_tensor(pool_np, device=DEV)
+        q = torch.randn(n_seqs, 4, 64, device=DEV, generator=gen)
+        bt = torch.as_tensor(table_array(tables), device=DEV)
+        ctx = torch.tensor(lens, dtype=torch.int32, device=DEV)
+        kp, vp = pool[0, 0], pool[0, 1]
+        ref = _oracle(q, kp, vp, bt, ctx, 0.125)
+        for name, got in (("v1", m1.paged_attention(q, kp, vp, bt, ctx, 0.125)),
+                          ("v2", m2.paged_attention_v2(q, kp, vp, bt, ctx, 0.125)),
+                          ("v3", m3.paged_attention_v3(q, kp, vp, bt, ctx, 0.125, 0))):
+            err = _maxerr(got, ref)
+            assert err < 5e-3, f"{name} trial {trial} lens={lens} bs={bs} err={err:.2e}"
+
+
+# ---------------------------------------------------------------------------
+# dtypes, head dims, block sizes, GQA, edge cases
+# ---------------------------------------------------------------------------
+
+
+def _random_case(lens, H, Hkv, D, bs, dtype, seed, nb_extra=8, shuffle=True):
+    rng = np.random.default_rng(seed)
+    need = sum(-(-n // bs) for n in lens)
+    nb = need + nb_extra
+    perm = rng.permutation(nb) if shuffle else np.arange(nb)
+    tables, i = [], 0
+    for n in lens:
+        k = -(-n // bs)
+        tables.append([int(x) for x in perm[i:i + k]])
+        i += k
+    gen = torch.Generator(device=DEV).manual_seed(seed)
+    pool = torch.randn((1, 2, nb, bs, Hkv, D), generator=gen, device=DEV).to(dtype)
+    q = torch.randn((len(lens), H, D), generator=gen, device=DEV)
+    bt = torch.as_tensor(table_array(tables), device=DEV)
+    ctx = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    return pool, q, bt, ctx
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("D", [32, 64, 128, 256])
+def test_decode_dtypes_and_head_dims(dtype, D):
+    """Every (dtype, head_dim) instantiation vs the oracle, 2e-3 max-abs."""
+    m1, m2, m3 = _mods()
+    lens = [1, 15, 16, 17, 100, 300]
+    pool, q, bt, ctx = _random_case(lens, 4, 4, D, 16, dtype, seed=D)
+    scale = D ** -0.5
+    kp, vp = pool[0, 0], pool[0, 1]
+    want = _oracle(q, kp, vp, bt, ctx, scale)
+    for got in (m1.paged_attention(q, kp, vp, bt, ctx, scale),
+                m2.paged_attention_v2(q, kp, vp, bt, ctx, scale),
+                m3.paged_attention_v3(q, kp, vp, bt, ctx, scale, 5)):
+        assert _maxerr(got, want) <= 2e-3
+
+
+@pytest.mark.parametrize("bs", [1, 2, 4, 8, 32])
+def test_decode_block_sizes(bs):
+    """Pages smaller than one wave-wide load take the per-lane addressing path."""
+    m1, _, m3 = _mods()
+    lens = [3, 64, 257, 600]
+    pool, q, bt, ctx = _random_case(lens, 4, 4, 64, bs, torch.float16, seed=100 + bs)
+    kp, vp = pool[0, 0], pool[0, 1]
+    want = _oracle(q, kp, vp, bt, ctx, 0.125)
+    assert _maxerr(m1.paged_attention(q, kp, vp, bt, ctx, 0.125), want) <= 2e-3
+    assert _maxerr(m3.paged_attention_v3(q, kp, vp, bt, ctx, 0.125, 3), want) <= 2e-3
+
+
+@pytest.mark.parametrize("H,Hkv", [(8, 2), (8, 1), (12, 4), (6, 6), (5, 5)])
+def test_decode_gqa_and_odd_head_counts(H, Hkv):
+    """GQA/MQA head mapping, and head counts that do not fill a 4-wave workgroup."""
+    m1, _, _ = _mods()
+    pool, q, bt, ctx = _random_case([40, 333], H, Hkv, 128, 16, torch.bfloat16, seed=H * 10 + Hkv)
+    kp, vp = pool[0, 0], pool[0, 1]
+    want = _oracle(q, kp, vp, bt, ctx, 128 ** -0.5)
+    assert _maxerr(m1.paged_attention(q, kp, vp, bt, ctx, 128 ** -0.5), want) <= 2e-3
+
+
+def test_zero_context_gives_zero_rows():
+    """ctx <= 0 is undefined in the reference (its kernels return without
+    writing, its torch path gives NaN); libhsattn defines it as a zero row."""
+    m1, m2, m3 = _mods()
+    pool, q, bt, ctx = _random_case([20, 5, 30], 4, 4, 64, 16, torch.float16, seed=3)
+    ctx[1] = 0
+    kp, vp = pool[0, 0], pool[0, 1]
+    want = _oracle(q, kp, vp, bt, ctx, 0.125)
+    for got in (m1.paged_attention(q, kp, vp, bt, ctx, 0.125),
+                m2.paged_attention_v2(q, kp, vp, bt, ctx, 0.125),
+                m3.paged_attention_v3(q, kp, vp, bt, ctx, 0.125, 4)):
+        g = got.cpu()
+        assert torch.all(g[1] == 0)
+        assert _maxerr(g[[0, 2]], want[[0, 2]]) <= 2e-3
+
+
+def test_context_beyond_table_and_negative_entries():
+    """ctx larger than the table holds is clamped to MB * BS, and -1 entries
+    inside the context read block 0 -- both as the torch reference does."""
+    m1, _, m3 = _mods()
+    pool, q, bt, ctx = _random_case([40, 64], 4, 4, 64, 16, torch.float16, seed=11)
+    ctx[0] = 10_000            # table has 3 blocks = 48 positions
+    bt[1, 2] = -1              # hole inside sequence 1's context
+    kp, vp = pool[0, 0], pool[0, 1]
+    want = _oracle(q, kp, vp, bt, ctx, 0.125)
+    for got in (m1.paged_attention(q, kp, vp, bt, ctx, 0.125),
+                m3.paged_attention_v3(q, kp, vp, bt, ctx, 0.125, 2)):
+        assert _maxerr(got, want) <= 2e-3
+
+
+def test_split_invariance_and_partition_sizes():
+    """The result may not depend on the decomposition: one pass, num_splits
+    slices and fixed partitions of several sizes all agree."""
+    from heteroserve import _hip
+
+    _mods()
+    pool, q, bt, ctx = _random_case([1, 255, 256, 257, 1000, 2500], 8, 8, 128, 16,
+                                    torch.bfloat16, seed=21)
+    kp, vp = pool[0, 0], pool[0, 1]
+    scale = 128 ** -0.5
+    want = _oracle(q, kp, vp, bt, ctx, scale)
+    outs = [_hip.decode(q, kp, vp, bt, ctx, scale, num_splits=s) for s in (1, 2, 3, 17, 64)]
+    outs += [_hip.decode(q, kp, vp, bt, ctx, scale, 0, partition_tokens=p)
+             for p in (16, 64, 256, 512, 4096)]
+    for o in outs:
+        assert _maxerr(o, want) <= 2e-3
+        assert _maxerr(o, outs[0]) <= 1e-4
+
+
+def test_errors_are_raised_with_reference_messages():
+    m1, m2, _ = _mods()
+    pool, q, bt, ctx = _random_case([10], 4, 4, 64, 16, torch.float16, seed=1)
+    kp, vp = pool[0, 0], pool[0, 1]
+    with pytest.raises(RuntimeError, match="q must be on CUDA"):
+        m1.paged_attention(q.cpu(), kp, vp, bt, ctx, 0.1)
+    with pytest.raises(RuntimeError, match="divisible"):
+        m2.paged_attention_v2(q[:, :3].contiguous(), kp[:, :, :2].contiguous(),
+                              vp[:, :, :2].contiguous(), bt, ctx, 0.1)
+    with pytest.raises(RuntimeError, match="head_dim"):
+        m1.paged_attention(q[..., :48].contiguous(), kp[..., :48].contiguous(),
+                           vp[..., :48].contiguous(), bt, ctx, 0.1)
+    with pytest.raises(RuntimeError, match="float32"):
+        m1.paged_attention(q.half(), kp, vp, bt, ctx, 0.1)
+
+
+# ---------------------------------------------------------------------------
+# benchmark configurations at full size
+# ---------------------------------------------------------------------------
+
+
+def _config(name):
+    from hsbench import cases
+
+    return cases.CONFIGS[name](DEV)
+
+
+def _check_sequences(case, got, seqs, tol):
+    kc, vc = case.k_cache, case.v_cache
+    for b in seqs:
+        n = int(case.ctx[b])
+        nblk = -(-n // 16)
+        blocks = case.block_tables[b, :nblk]
+        kb = kc.index_select(0, blocks.long()).cpu()
+        vb = vc.index_select(0, blocks.long()).cpu()
+        want = decode_one(case.q[b].cpu(), kb, vb, torch.arange(nblk, dtype=torch.int32),
+                          n, case.scale)
+        err = _maxerr(got[b], want)
+        assert err <= tol, f"{case.name} sequence {b} ctx {n}: max err {err:.2e}"
+
+
+def test_c1_full_batch_against_the_oracle():
+    m1, _, m3 = _mods()
+    case = _config("C1")
+    want = _oracle(case.q, case.k_cache, case.v_cache, case.block_tables, case.context_lens,
+                   case.scale)
+    for got in (m1.paged_attention(case.q, case.k_cache, case.v_cache, case.block_tables,
+                                   case.context_lens, case.scale),
+                m3.paged_attention_v3(case.q, case.k_cache, case.v_cache, case.block_tables,
+                                      case.context_lens, case.scale, 8)):
+        assert _maxerr(got, want) <= 2e-3
+
+
+@pytest.mark.parametrize("name", ["C2", "C3", "C5-decode"])
+def test_large_configs(name):
+    """Full-size batches: a seeded sample of sequences (shortest, longest and
+    random ones) against the per-sequence oracle at 2e-3, and the whole batch
+    through the decomposition-invariance property."""
+    m1, m2, m3 = _mods()
+    case = _config(name)
+    args = (case.q, case.k_cache, case.v_cache, case.block_tables, case.context_lens,
+            case.scale)
+    fast = m1.paged_attention(*args)
+    rng = np.random.default_rng(99)
+    sample = {int(np.argmin(case.ctx)), int(np.argmax(case.ctx))}
+    sample |= set(rng.choice(len(case.ctx), size=3, replace=False).tolist())
+    _check_sequences(case, fast, sorted(sample), 2e-3)
+    one_pass = m2.paged_attention_v2(*args)
+    split = m3.paged_attention_v3(*args, 13)
+    assert _maxerr(fast, one_pass) <= 2e-3
+    assert _maxerr(fast, split) <= 2e-3
+    assert torch.isfinite(fast).all()
+    del case
+    torch.cuda.empty_cache()

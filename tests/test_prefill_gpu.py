@@ -1,0 +1,212 @@
+"""GPU parity of the causal prefill kernels against the oracle.
+
+Restates the reference's gates (tests/test_torch_engine.py:549-589 for the
+scalar kernel, :656-699 for the tensor-core kernel) on libhsattn: the fp32
+row kernel behind ``paged_attention_prefill`` and the MFMA kernel behind
+``paged_attention_prefill_wmma``.  The north-star tolerance for fp16/bf16
+caches is a 2e-3 max-abs error, tighter than the reference's 2e-2 WMMA gate.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+from _refcases import lay_out, prefill_case, table_array  # noqa: E402
+from oracle.attention import decode_one, paged_attention_prefill_torch, prefill_one  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def _maxerr(a, b) -> float:
+    return (a.detach().float().cpu() - b.detach().float().cpu()).abs().max().item()
+
+
+def _oracle(q, k, v, bt, ctx, scale):
+    return paged_attention_prefill_torch(q.cpu(), k.cpu(), v.cpu(), bt.cpu(), ctx.cpu(), scale)
+
+
+def _ref_prefill(lens, S, kvh, seed, dtype=torch.float32):
+    c = prefill_case(lens, S, kvh, seed=seed)
+    pool = torch.as_tensor(c["pool"]).to(DEV, dtype)
+    bt = torch.as_tensor(table_array(c["tables"]), device=DEV)
+    ctx = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    q = torch.as_tensor(c["q"], device=DEV)
+    return pool, bt, ctx, q, c["scale"]
+
+
+def test_prefill_kernel_matches_reference():
+    """tests/test_torch_engine.py:549-567 (fp32 KV, seed = S), 1e-3."""
+    from heteroserve.model import paged_attn_prefill as pf
+
+    assert pf.is_available(), pf.build_error()
+    for lens, S, kvh in [([64], 64, None), ([37, 64, 19], 16, None), ([64], 32, 2),
+                         ([48], 48, 1)]:
+        pool, bt, ctx, q, scale = _ref_prefill(lens, S, kvh, seed=S)
+        got = pf.paged_attention_prefill(q, pool[0, 0], pool[0, 1], bt, ctx, scale)
+        want = _oracle(q, pool[0, 0], pool[0, 1], bt, ctx, scale)
+        np.testing.assert_allclose(got.cpu().numpy(), want.numpy(), rtol=1e-3, atol=1e-3,
+                                   err_msg=f"lens={lens} S={S} kv={kvh}")
+
+
+def test_prefill_with_one_query_equals_decode():
+    """tests/test_torch_engine.py:570-589: S = 1 prefill == v2 decode, 1e-3."""
+    from heteroserve.model import paged_attn_prefill as pf
+    from heteroserve.model import paged_attn_v2 as v2
+
+    pool, bt, ctx, q, scale = _ref_prefill([31, 64, 17], 1, None, seed=3)
+    pre = pf.paged_attention_prefill(q, pool[0, 0], pool[0, 1], bt, ctx, scale)
+    dec = v2.paged_attention_v2(q[:, 0].contiguous(), pool[0, 0], pool[0, 1], bt, ctx, scale)
+    np.testing.assert_allclose(pre[:, 0].cpu().numpy(), dec.cpu().numpy(), rtol=1e-3, atol=1e-3)
+
+
+def test_prefill_padded_rows_are_zero():
+    """A sequence shorter than the chunk has leading rows at negative
+    positions: they attend to nothing and are 0 (paged_attn_prefill.py:321)."""
+    from heteroserve.model import paged_attn_prefill as pf
+
+    pool, bt, ctx, q, scale = _ref_prefill([64, 10], 32, None, seed=5)
+    got = pf.paged_attention_prefill(q, pool[0, 0], pool[0, 1], bt, ctx, scale).cpu()
+    assert torch.all(got[1, :22] == 0)
+    want = _oracle(q, pool[0, 0], pool[0, 1], bt, ctx, scale)
+    assert _maxerr(got, want) <= 1e-3
+
+
+# ---------------------------------------------------------------------------
+# matrix-core path
+# ---------------------------------------------------------------------------
+
+
+def _wmma():
+    from heteroserve.model import paged_attn_wmma as wm
+
+    assert wm.is_available(), wm.build_error()
+    return wm
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_mfma_matches_the_scalar_reference(dtype):
+    """tests/test_torch_engine.py:656-699 with the north-star 2e-3 bound
+    (the reference gates its WMMA kernel at 2e-2)."""
+    wm = _wmma()
+    for lens, S, kvh in [([64], 64, None), ([37, 64, 19], 16, None), ([64], 32, 2)]:
+        hkv = kvh or 4
+        rng = np.random.default_rng(S + len(lens))
+        seqs = []
+        for n in lens:
+            rng.integers(1, 4000, size=n)
+            k = rng.standard_normal((4, hkv, n, 64)).astype(np.float16)
+            seqs.append((k, k))
+        pool_np, tables = lay_out(seqs, 16, 96, hkv, np.float16)
+        pool = torch.as_tensor(pool_np, device=DEV).to(dtype)
+        assert wm.supports(16, 64, pool.dtype)
+        gen = torch.Generator(device=DEV).manual_seed(S)
+        q = torch.randn(len(lens), S, 4, 64, device=DEV, generator=gen)
+        bt = torch.as_tensor(table_array(tables), device=DEV)
+        ctx = torch.tensor(lens, dtype=torch.int32, device=DEV)
+        got = wm.paged_attention_prefill_wmma(q, pool[0, 0], pool[0, 1], bt, ctx, 0.125)
+        want = _oracle(q, pool[0, 0], pool[0, 1], bt, ctx, 0.125)
+        err = _maxerr(got, want)
+        assert err <= 2e-3, f"lens={lens} S={S} kv={kvh} err={err:.2e}"
+
+
+@pytest.mark.parametrize("ctx_len,S,D", [
+    (64, 32, 64), (64, 19, 64), (57, 16, 64), (91, 23, 64), (48, 48, 64), (80, 1, 64),
+    (100, 40, 128), (512, 16, 64), (300, 300, 32), (1000, 129, 128), (2048, 700, 128),
+])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_mfma_misaligned_shapes(ctx_len, S, D, dtype):
+    """The tile-loop cases of tests/test_torch_engine.py:610-619 (plus larger
+    ones) run on the GPU kernel: chunks and contexts that are not multiples of
+    the tile, one query row, S == ctx, all three head dims."""
+    wm = _wmma()
+    rng = np.random.default_rng(ctx_len * 31 + S)
+    nb = -(-ctx_len // 16) + 5
+    perm = rng.permutation(nb)
+    table = [int(x) for x in perm[: -(-ctx_len // 16)]]
+    gen = torch.Generator(device=DEV).manual_seed(ctx_len + S + D)
+    pool = torch.randn((1, 2, nb, 16, 2, D), generator=gen, device=DEV).to(dtype)
+    q = torch.randn((1, S, 4, D), generator=gen, device=DEV)
+    bt = torch.as_tensor(table_array([table]), device=DEV)
+    ctx = torch.tensor([ctx_len], dtype=torch.int32, device=DEV)
+    got = wm.paged_attention_prefill_wmma(q, pool[0, 0], pool[0, 1], bt, ctx, D ** -0.5)
+    want = _oracle(q, pool[0, 0], pool[0, 1], bt, ctx, D ** -0.5)
+    assert _maxerr(got, want) <= 2e-3
+
+
+def test_mfma_with_one_query_equals_decode():
+    wm = _wmma()
+    from heteroserve.model import paged_attn_v2 as v2
+
+    pool, bt, ctx, q, scale = _ref_prefill([31, 64, 17], 1, None, seed=3, dtype=torch.float16)
+    pre = wm.paged_attention_prefill_wmma(q, pool[0, 0], pool[0, 1], bt, ctx, scale)
+    dec = v2.paged_attention_v2(q[:, 0].contiguous(), pool[0, 0], pool[0, 1], bt, ctx, scale)
+    assert _maxerr(pre[:, 0], dec) <= 2e-3
+
+
+def test_mfma_rejects_what_it_cannot_serve():
+    wm = _wmma()
+    assert wm.supports(32, 64, torch.float16) is False
+    assert wm.supports(16, 64, torch.float32) is False
+    assert wm.supports(16, 48, torch.float16) is False
+    pool = torch.zeros((1, 2, 4, 16, 4, 64), device=DEV)
+    q = torch.zeros((1, 4, 4, 64), device=DEV)
+    bt = torch.zeros((1, 4), dtype=torch.int32, device=DEV)
+    ctx = torch.tensor([8], dtype=torch.int32, device=DEV)
+    with pytest.raises(RuntimeError, match="fp16 or bf16"):
+        wm.paged_attention_prefill_wmma(q, pool[0, 0], pool[0, 1], bt, ctx, 0.1)
+
+
+def test_varlen_matches_per_sequence_calls():
+    """One ragged launch == B = 1 calls per chunk (the engine's pattern,
+    torch_engine.py:292-313), for both kernels."""
+    from heteroserve.model import paged_attn_prefill as pf
+
+    _wmma()
+    from hsbench.cases import build_prefill
+
+    case = build_prefill("t", np.array([0, 33, 500, 16]), np.array([40, 1, 129, 300]),
+                         8, 4, 128, 200, torch.bfloat16, DEV, seed=8)
+    cu = case.cu_seqlens.cpu().numpy()
+    for mfma in (False, True):
+        got = pf.paged_attention_prefill_varlen(case.q, case.cu_seqlens, int(case.q_lens.max()),
+                                                case.k_cache, case.v_cache, case.block_tables,
+                                                case.context_lens, case.scale, use_mfma=mfma)
+        for b in range(4):
+            qb = case.q[cu[b]:cu[b + 1]]
+            want = prefill_one(qb.cpu(), case.k_cache.cpu(), case.v_cache.cpu(),
+                               case.block_tables[b].cpu(), int(case.ctx[b]), case.scale)
+            assert _maxerr(got[cu[b]:cu[b + 1]], want) <= 2e-3, (mfma, b)
+
+
+@pytest.mark.parametrize("name", ["C4", "C5-prefill"])
+def test_prefill_configs(name):
+    """Full-size chunked prefill through the MFMA kernel: every sequence's
+    rows against the per-sequence oracle on a sample of rows, 2e-3."""
+    from heteroserve.model import paged_attn_prefill as pf
+    from hsbench import cases
+
+    _wmma()
+    case = cases.CONFIGS[name](DEV)
+    got = pf.paged_attention_prefill_varlen(case.q, case.cu_seqlens, int(case.q_lens.max()),
+                                            case.k_cache, case.v_cache, case.block_tables,
+                                            case.context_lens, case.scale, use_mfma=True)
+    assert torch.isfinite(got).all()
+    cu = case.cu_seqlens.cpu().numpy()
+    rng = np.random.default_rng(5)
+    for b in range(len(case.ctx)):
+        S_b, n = int(case.q_lens[b]), int(case.ctx[b])
+        rows = sorted({0, S_b - 1, *rng.integers(0, S_b, size=6).tolist()})
+        nblk = -(-n // 16)
+        blocks = case.block_tables[b, :nblk].long()
+        kb = case.k_cache.index_select(0, blocks).cpu()
+        vb = case.v_cache.index_select(0, blocks).cpu()
+        local = torch.arange(nblk, dtype=torch.int32)
+        for r in rows:
+            pos = n - S_b + r          # the row attends to keys [0, pos]
+            want = decode_one(case.q[cu[b] + r].cpu(), kb, vb, local, pos + 1, case.scale)
+            err = _maxerr(got[cu[b] + r], want)
+            assert err <= 2e-3, f"{name} seq {b} row {r}: err {err:.2e}"
