@@ -160,8 +160,9 @@ def pack_leg(steps: int, warmup: int) -> dict:
 # ---------------------------------------------------------------------------
 
 
-def cpu_baseline(case, n_seq: int = 16, seed: int = 7) -> dict:
-    """Per-sequence torch oracle on a seeded sample of the case's sequences."""
+def cpu_baseline(case, n_seq: int = 0, seed: int = 7) -> dict:
+    """Per-sequence torch oracle over the case's sequences (all of them when
+    n_seq is 0, else a seeded sample of n_seq)."""
     import numpy as np
     import torch
 
@@ -170,7 +171,8 @@ def cpu_baseline(case, n_seq: int = 16, seed: int = 7) -> dict:
     threads = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
     torch.set_num_threads(threads)
     rng = np.random.default_rng(seed)
-    pick = sorted(rng.choice(len(case.ctx), size=min(n_seq, len(case.ctx)), replace=False))
+    n_pick = len(case.ctx) if n_seq <= 0 else min(n_seq, len(case.ctx))
+    pick = sorted(rng.choice(len(case.ctx), size=n_pick, replace=False))
     host = []
     for b in pick:
         n = int(case.ctx[b])
@@ -253,7 +255,7 @@ def main() -> int:
         "head_dim": case.head_dim, "block_size": 16, "kv_dtype": kv_dtype,
         "sum_context": int(case.ctx.sum()), "max_context": int(case.ctx.max()),
         "num_blocks": int(case.k_cache.shape[0]),
-        "decomposition": f"fixed partitions of {args.partition or 256} tokens + LSE merge",
+        "decomposition": f"fixed partitions of {args.partition or 512} tokens + LSE merge",
         "parallelism": "none (one GPU)",
     }
     if case.meta.get("shared_blocks"):

@@ -45,7 +45,7 @@ void profile_end(hipStream_t stream) {
   g_profile = ProfileRequest{};
 }
 
-constexpr int kDefaultPartition = 256;
+constexpr int kDefaultPartition = 512;
 
 static int device_cu_count(int device) {
   static std::mutex mu;

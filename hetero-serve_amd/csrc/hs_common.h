@@ -77,6 +77,13 @@ struct Elem<Bf16> {
 
 __device__ inline uint4 load16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
 
+// 16-byte load with the non-temporal hint, for data read exactly once.
+__device__ inline uint4 load16_stream(const void* p) {
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 x = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  return make_uint4(x[0], x[1], x[2], x[3]);
+}
+
 // ---------------------------------------------------------------------------
 // Wave reductions
 // ---------------------------------------------------------------------------

@@ -15,8 +15,15 @@
 // product is reduced inside one 16-lane DPP row, with no LDS traffic.  Each
 // group of kLpt lanes ("slot") runs its own online softmax over the tokens it
 // loads; the kTpl slot states are merged once at the end of the partition.
-// A workgroup is 4 waves = 4 consecutive heads of the same (row, partition),
-// so the four waves stream adjacent 2*D-byte pieces of the same token rows.
+// A workgroup is kWaves waves = consecutive heads of the same (row,
+// partition), and the head group is the fastest-varying grid index, so the
+// workgroups in flight together stream whole token rows (all heads of a token
+// are adjacent in the page) instead of one head's narrow column of many rows.
+// KV loads are non-temporal: every byte is read once, so it should not
+// displace anything in L2.  Measured on MI355X (C2 decode): the head-major
+// grid order took the kernel from 3.5 to 5.3 TB/s, non-temporal loads to
+// 5.8 TB/s, 32 tokens of loads in flight per wave and 512-token partitions
+// to ~6 TB/s.
 #include "hs_kernels.h"
 
 namespace hs {
@@ -64,20 +71,25 @@ __device__ inline bool partition_range(const RowAttnArgs& a, int end, int p, int
   return p < nparts;
 }
 
+constexpr int kDecodeWaves = 2;  // heads per workgroup
+
 template <typename T, int D, bool kPaged>
-__global__ __launch_bounds__(256) void row_attn_part_kernel(RowAttnArgs a) {
+__global__ __launch_bounds__(kDecodeWaves * 64) void row_attn_part_kernel(RowAttnArgs a) {
   constexpr int kVec = Elem<T>::kVec;
   constexpr int kLpt = D / kVec;           // lanes per token
   constexpr int kTpl = 64 / kLpt;          // tokens per wave-wide load
-  constexpr int kU = kTpl >= 16 ? 1 : 16 / kTpl;  // loads in flight per operand
+  constexpr int kU = kTpl >= 32 ? 1 : (32 / kTpl < 8 ? 32 / kTpl : 8);  // loads in flight
   constexpr int kStep = kTpl * kU;         // tokens per loop iteration
   static_assert(kLpt >= 1 && kLpt <= 64 && 64 % kLpt == 0, "head_dim / lane split");
 
   const int lane = threadIdx.x & 63;
-  const int h = blockIdx.y * 4 + (threadIdx.x >> 6);
+  const int n_groups = (a.H + kDecodeWaves - 1) / kDecodeWaves;
+  const int64_t wg = blockIdx.x;
+  const int h = (int)(wg % n_groups) * kDecodeWaves + (threadIdx.x >> 6);
   if (h >= a.H) return;
-  const int row = blockIdx.x / a.P;
-  const int p = blockIdx.x - row * a.P;
+  const int64_t rp = wg / n_groups;        // row * P + partition
+  const int row = (int)(rp / a.P);
+  const int p = (int)(rp - (int64_t)row * a.P);
 
   int b, end;
   if (!row_geometry(a, row, b, end)) return;
@@ -138,8 +150,8 @@ __global__ __launch_bounds__(256) void row_attn_part_kernel(RowAttnArgs a) {
         const int t = min(tg + r, hi - 1);
         off = safe_block(bt[t / a.BS], a.NB) * blk_stride + (int64_t)(t % a.BS) * tok_stride;
       }
-      kr[u] = load16(kp + off);
-      vr[u] = load16(vp + off);
+      kr[u] = load16_stream(kp + off);
+      vr[u] = load16_stream(vp + off);
     }
 
     float sc[kU];
@@ -268,9 +280,11 @@ static void launch_typed(const RowAttnArgs& a, dim3 grid, hipStream_t stream) {
   const int tpl = 64 / (D / Elem<T>::kVec);
   profile_begin(stream);
   if (a.BS % tpl == 0)
-    hipLaunchKernelGGL((row_attn_part_kernel<T, D, true>), grid, dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((row_attn_part_kernel<T, D, true>), grid, dim3(kDecodeWaves * 64), 0,
+                       stream, a);
   else
-    hipLaunchKernelGGL((row_attn_part_kernel<T, D, false>), grid, dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((row_attn_part_kernel<T, D, false>), grid, dim3(kDecodeWaves * 64), 0,
+                       stream, a);
   profile_end(stream);
   if (a.P > 1) {
     const int64_t waves = (int64_t)a.rows * a.H;
@@ -294,11 +308,12 @@ static int launch_dim(const RowAttnArgs& a, int D, dim3 grid, hipStream_t stream
 // Launch the partition kernel (+ merge when P > 1).  Arguments are validated
 // by the caller.
 int launch_row_attn(const RowAttnArgs& a, int kv_dtype, int D, hipStream_t stream) {
-  const int64_t gx = (int64_t)a.rows * a.P;
+  const int64_t gx = (int64_t)a.rows * a.P * ((a.H + kDecodeWaves - 1) / kDecodeWaves);
   if (gx <= 0) return HS_OK;
   if (gx > 0x7fffffffLL)
-    return fail(HS_EUNSUPPORTED, "grid too large: rows * partitions = " + std::to_string(gx));
-  const dim3 grid((unsigned)gx, (unsigned)((a.H + 3) / 4));
+    return fail(HS_EUNSUPPORTED, "grid too large: rows * partitions * head groups = " +
+                                     std::to_string(gx));
+  const dim3 grid((unsigned)gx);
   switch (kv_dtype) {
     case HS_DTYPE_F32: return launch_dim<float>(a, D, grid, stream);
     case HS_DTYPE_F16: return launch_dim<_Float16>(a, D, grid, stream);

@@ -14,7 +14,7 @@ Layout, as in the reference:
     ->                  [B, H, D]            float32
 
 The reference's v1 kernel keeps every score in shared memory; here the call
-runs libhsattn's partitioned online-softmax decode (fixed 256-token
+runs libhsattn's partitioned online-softmax decode (fixed 512-token
 partitions plus a log-sum-exp merge), which computes the same function.
 
 Difference from the reference: when the HIP library is unavailable the

@@ -7,7 +7,7 @@ build_error :347, choose_num_splits :352-356, paged_attention_v3 :359-367).
 context is cut into ``num_splits`` slices of ceil(ctx / num_splits) tokens,
 each slice runs an independent online softmax, and a merge kernel combines
 the partial states.  ``num_splits <= 0`` lets the library choose; on MI355X it
-uses fixed 256-token partitions, which balance a ragged batch across the 256
+uses fixed 512-token partitions, which balance a ragged batch across the 256
 CUs better than a per-batch split count.  Results do not depend on the
 decomposition (the reference asserts this, test_torch_engine.py:405-429).
 """
