@@ -47,6 +47,24 @@ def log(*a) -> None:
     print(*a, file=sys.stderr, flush=True)
 
 
+# HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE, WRITE_SIZE,
+# calibrated on a 1 GiB copy) for the default workload; summarised in the
+# committed profile below, whose table this reads.
+TRAFFIC_PROFILE = ROOT / "profiles" / "decode_C2_prefill_C4_pack_C5.md"
+
+
+def profiled_traffic(kernel: str):
+    """HBM read + write bytes of `kernel` from the committed PMC summary."""
+    try:
+        for line in TRAFFIC_PROFILE.read_text().splitlines():
+            cells = [c.strip(" `") for c in line.split("|")]
+            if len(cells) == 7 and cells[1] == kernel and "." in cells[4]:
+                return int(round((float(cells[4]) + float(cells[5])) * 1e9))
+    except (OSError, ValueError):
+        pass
+    return None
+
+
 # ---------------------------------------------------------------------------
 # GPU legs
 # ---------------------------------------------------------------------------
@@ -312,7 +330,9 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(dec["kernel_gbs"] / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": profiled_traffic("hs::row_attn_part_kernel<hs::Bf16, 128, true>")
+            if args.config == "C2" and not args.partition else None,
+            "traffic_source": TRAFFIC_PROFILE.name,
             "algorithmic_bytes": dec["bytes"],
             "kernel_us": round(dec["kernel_ms"] * 1e3, 2),
         },
