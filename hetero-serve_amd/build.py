@@ -51,9 +51,20 @@ COMPILE_FLAGS = [
 ]
 
 
+# Per-source flags.  The MFMA prefill kernel holds more live state than the
+# 256 architectural VGPRs; LLVM's default then keeps MFMA accumulators in
+# VGPRs and spills other values to AGPRs, reloading them every loop
+# iteration.  Forcing the VGPR form for MFMA operands cut the loop's
+# instruction count by ~45% (measured on the generated gfx950 code).
+PER_FILE_FLAGS = {
+    "hs_prefill_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=true"],
+}
+
+
 def _compile(src: Path, extra: list[str]) -> Path:
     obj = BUILD_DIR / (src.stem + ".o")
-    cmd = [hipcc(), *COMPILE_FLAGS, *extra, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *COMPILE_FLAGS, *PER_FILE_FLAGS.get(src.name, []), *extra, "-c", str(src),
+           "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"
     msgs = [ln for ln in (res.stdout + res.stderr).splitlines() if noise not in ln]

@@ -219,7 +219,9 @@ static int prefill_common(const float* q, const int32_t* cu_q, int S, int max_ro
       return fail(HS_EUNSUPPORTED, "the MFMA path needs block_size == 16 (one page per tile)");
     if (!(D == 32 || D == 64 || D == 128))
       return fail(HS_EUNSUPPORTED, "unsupported head_dim for the MFMA path: " + std::to_string(D));
-    return launch_prefill_mfma(q, cu_q, S, max_rows, k_cache, v_cache, kv_dtype, num_blocks,
+    // S is the rows of every sequence (padded form) or the longest sequence's
+    // rows (ragged form): the MFMA grid is sized per sequence.
+    return launch_prefill_mfma(q, cu_q, S, S, k_cache, v_cache, kv_dtype, num_blocks,
                                block_tables, context_lens, out, B, H, Hkv, D, BS, MB, scale, st);
   }
   if (!valid_row_head_dim(D))
