@@ -129,126 +129,141 @@ __device__ inline uint4 to_f16x8<_Float16>(const uint4& w) {
   return w;
 }
 
-// One thread's share of a K/V tile in flight from global memory.
-//   K: chunk c = tid + 256*u is key c / (D/8), dims 8*(c % (D/8)): 16
-//      neighbouring lanes read one 256-byte head row.
+// Element e of two chunks, as the fp16 pair (x[e], y[e]).
+template <typename T>
+__device__ inline uint32_t pack_col(const uint4& x, const uint4& y, int e) {
+  return pack_f16(elem_f32<T>(x, e), elem_f32<T>(y, e));
+}
+
+template <>
+__device__ inline uint32_t pack_col<_Float16>(const uint4& x, const uint4& y, int e) {
+  const uint32_t xw = e < 2 ? x.x : e < 4 ? x.y : e < 6 ? x.z : x.w;
+  const uint32_t yw = e < 2 ? y.x : e < 4 ? y.y : e < 6 ? y.z : y.w;
+  // v_perm_b32: bytes {x half, y half} of the selected 16-bit lanes
+  return __builtin_amdgcn_perm(yw, xw, (e & 1) ? 0x07060302u : 0x05040100u);
+}
+
+// Both lane halves' values of x: {lanes 0-31, lanes 32-63} seen from each lane.
+__device__ inline float sum_halves(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+__device__ inline float max_halves(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+// The producer: how the 256 threads of a workgroup move one K/V tile from
+// the paged cache through registers into LDS.
+//   K: chunk c = tid + 256*u is key c / (D/8), dims 8*(c % (D/8)).  16
+//      neighbouring lanes read one 256-byte head row, and every load of a
+//      wave falls in a single page, so the page base is a scalar and each lane
+//      keeps one 32-bit offset for the whole walk.
 //   V: the thread owns kG consecutive keys kG*(tid % (64/kG)) of the 8 dims
 //      8*(tid / (64/kG)), so that its transposed LDS store for one dim is one
 //      kG*2-byte write and 64/kG neighbouring lanes fill one V^T row segment.
+//      Its kG keys lie in one page: one block id and one base per tile.
+// The four block ids of a tile are fetched by one vector load (lane L reads
+// the id of the page its V keys are in); K page p's id is read from the lane
+// that holds it.
 template <int D>
-struct TileRegs {
-  static constexpr int kKChunks = kBN * D / 8 / kThreads;  // D=128: 4
-  static constexpr int kG = kKChunks;                      // keys per thread in V
+struct Producer {
+  static constexpr int kDC = D / 8;                         // 16-byte chunks per head row
+  static constexpr int kKChunks = kBN * D / 8 / kThreads;   // K chunks per thread (D=128: 4)
+  static constexpr int kG = kKChunks;                       // V keys per thread
+  static constexpr int kGroups = kBN / kG;                  // V key groups per dim chunk
+  static constexpr int kKeysPerU = kThreads / kDC;          // keys between K chunks u, u+1
+  static constexpr int kPages = kBN / 16;
   static_assert(kKChunks >= 1 && (kG == 1 || kG == 2 || kG == 4), "tile / thread split");
+  static_assert(kKeysPerU % 16 == 0 && 16 % kG == 0, "loads must not straddle pages");
   static constexpr int kChunksPerBlock = (kKChunks + kBN / 32 - 1) / (kBN / 32);
-  uint4 k[kKChunks];
+
+  uint4 k[kKChunks];   // tile in flight
   uint4 v[kG];
-};
+  int id;              // block id of page (this lane's V page) of the tile being fetched
 
-// Block ids of the pages a thread's loads of tile kt touch, fetched one tile
-// ahead of the loads themselves so that the block-table round trip never
-// sits in front of the K/V loads.
-template <int D>
-struct TileIds {
-  int k[TileRegs<D>::kKChunks];
-  int v[TileRegs<D>::kG];
-};
+  // per-thread constants
+  uint32_t koff;       // byte offset of this lane's K chunk inside a page (+ head)
+  int kpage0;          // page of K chunk 0 (wave-uniform)
+  int vpage;           // page of this lane's V keys
+  int64_t voff;        // element offset of this lane's V chunk inside a page (+ head)
+  int64_t tok;         // elements between consecutive tokens of a page
 
-template <int D>
-__device__ inline void tile_ids(const PrefillArgs& a, TileIds<D>& ids, const int32_t* bt, int kt) {
-  constexpr int kDC = D / 8;
-  constexpr int kG = TileRegs<D>::kG;
-  constexpr int kGroups = kBN / kG;
-  const int tid = threadIdx.x;
-#pragma unroll
-  for (int u = 0; u < TileRegs<D>::kKChunks; ++u) {
-    const int key = (tid + kThreads * u) / kDC;
-    ids.k[u] = bt[min(kt * (kBN / 16) + key / 16, a.MB - 1)];
+  __device__ inline void init(const PrefillArgs& a, int wave, int kvh) {
+    const int tid = threadIdx.x;
+    tok = (int64_t)a.Hkv * D;
+    const int t_k = tid / kDC;
+    koff = (uint32_t)(((t_k % 16) * tok + kvh * D + (tid % kDC) * 8) * 2);
+    kpage0 = wave * 64 / (16 * kDC);
+    const int key0 = kG * (tid % kGroups);
+    vpage = key0 / 16;
+    voff = (key0 % 16) * tok + kvh * D + (tid / kGroups) * 8;
   }
-#pragma unroll
-  for (int g = 0; g < kG; ++g) {
-    const int key = kG * (tid % kGroups) + g;
-    ids.v[g] = bt[min(kt * (kBN / 16) + key / 16, a.MB - 1)];
+
+  __device__ inline void fetch_ids(const PrefillArgs& a, const int32_t* bt, int kt) {
+    id = bt[min(kt * kPages + vpage, a.MB - 1)];
   }
-}
 
-template <typename T, int D>
-__device__ inline void load_k_chunk(const PrefillArgs& a, TileRegs<D>& r, const TileIds<D>& ids,
-                                    int kvh, int u) {
-  constexpr int kDC = D / 8;
-  const int c = threadIdx.x + kThreads * u;
-  const int key = c / kDC;
-  const int64_t tok = (int64_t)a.Hkv * D;
-  const int64_t off = safe_block(ids.k[u], a.NB) * tok * 16 + (key % 16) * tok + kvh * D +
-                      (c % kDC) * 8;
-  r.k[u] = load16(reinterpret_cast<const T*>(a.k) + off);
-}
-
-template <typename T, int D>
-__device__ inline void load_v(const PrefillArgs& a, TileRegs<D>& r, const TileIds<D>& ids,
-                              int kvh) {
-  constexpr int kG = TileRegs<D>::kG;
-  constexpr int kGroups = kBN / kG;
-  const int key0 = kG * (threadIdx.x % kGroups);
-  const int dc = threadIdx.x / kGroups;
-  const int64_t tok = (int64_t)a.Hkv * D;
-#pragma unroll
-  for (int g = 0; g < kG; ++g) {
-    const int key = key0 + g;
-    const int64_t off = safe_block(ids.v[g], a.NB) * tok * 16 + (key % 16) * tok + kvh * D +
-                        dc * 8;
-    r.v[g] = load16(reinterpret_cast<const T*>(a.v) + off);
+  template <typename T>
+  __device__ inline void load_k_chunk(const PrefillArgs& a, int u) {
+    const int page = kpage0 + u * (kKeysPerU / 16);              // wave-uniform
+    const int kid = __builtin_amdgcn_readlane(id, page * 16 / kG);
+    const char* base = reinterpret_cast<const char*>(a.k) +
+                       safe_block(kid, a.NB) * tok * 16 * (int64_t)sizeof(T);
+    k[u] = load16(base + koff);
   }
-}
 
-template <typename T, int D>
-__device__ inline void load_tile(const PrefillArgs& a, TileRegs<D>& r, const TileIds<D>& ids,
-                                 int kvh) {
+  template <typename T>
+  __device__ inline void load_v(const PrefillArgs& a) {
+    const T* p = reinterpret_cast<const T*>(a.v) + safe_block(id, a.NB) * tok * 16 + voff;
 #pragma unroll
-  for (int u = 0; u < TileRegs<D>::kKChunks; ++u) load_k_chunk<T, D>(a, r, ids, kvh, u);
-  load_v<T, D>(a, r, ids, kvh);
-}
+    for (int g = 0; g < kG; ++g) v[g] = load16(p + g * tok);
+  }
 
-// Registers -> LDS (fp16; K with the bit-2/3 row swap, V transposed).
-template <typename T, int D>
-__device__ inline void store_k_chunk(PrefillTileLds<D>& s, const TileRegs<D>& r, int u) {
-  constexpr int kDC = D / 8;
-  const int c = threadIdx.x + kThreads * u;
-  const int key = c / kDC;
-  const int row = (key & ~31) | swap_bits23(key & 31);
-  *reinterpret_cast<uint4*>(&s.k[row][(c % kDC) * 8]) = to_f16x8<T>(r.k[u]);
-}
-
-// V^T: the thread owns kG consecutive keys of 8 dims, so each of its 8
-// stores (one per dim) is a kG*2-byte write, and the kBN/kG lanes that share
-// a dim chunk fill one contiguous V^T row segment.
-template <typename T, int D>
-__device__ inline void store_v(PrefillTileLds<D>& s, const TileRegs<D>& r) {
-  constexpr int kG = TileRegs<D>::kG;
-  constexpr int kGroups = kBN / kG;
-  const int key0 = kG * (threadIdx.x % kGroups);
-  const int dc = threadIdx.x / kGroups;
+  template <typename T>
+  __device__ inline void load_tile(const PrefillArgs& a) {
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    _Float16* dst = &s.vt[dc * 8 + e][key0];
-    if constexpr (kG == 4) {
-      *reinterpret_cast<uint2*>(dst) =
-          make_uint2(pack_f16(elem_f32<T>(r.v[0], e), elem_f32<T>(r.v[1], e)),
-                     pack_f16(elem_f32<T>(r.v[2], e), elem_f32<T>(r.v[3], e)));
-    } else if constexpr (kG == 2) {
-      *reinterpret_cast<uint32_t*>(dst) = pack_f16(elem_f32<T>(r.v[0], e), elem_f32<T>(r.v[1], e));
-    } else {
-      *dst = (_Float16)elem_f32<T>(r.v[0], e);
+    for (int u = 0; u < kKChunks; ++u) load_k_chunk<T>(a, u);
+    load_v<T>(a);
+  }
+
+  // Registers -> LDS (fp16; K with the bit-2/3 row swap, V transposed).
+  template <typename T>
+  __device__ inline void store_k_chunk(PrefillTileLds<D>& s, int u) const {
+    const int t_k = threadIdx.x / kDC;
+    const int row0 = (t_k & ~31) | swap_bits23(t_k & 31);
+    *reinterpret_cast<uint4*>(&s.k[row0 + u * kKeysPerU][(threadIdx.x % kDC) * 8]) =
+        to_f16x8<T>(k[u]);
+  }
+
+  template <typename T>
+  __device__ inline void store_v(PrefillTileLds<D>& s) const {
+    const int key0 = kG * (threadIdx.x % kGroups);
+    const int dc = threadIdx.x / kGroups;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      _Float16* dst = &s.vt[dc * 8 + e][key0];
+      if constexpr (kG == 4) {
+        *reinterpret_cast<uint2*>(dst) =
+            make_uint2(pack_col<T>(v[0], v[1], e), pack_col<T>(v[2], v[3], e));
+      } else if constexpr (kG == 2) {
+        *reinterpret_cast<uint32_t*>(dst) = pack_col<T>(v[0], v[1], e);
+      } else {
+        *dst = (_Float16)elem_f32<T>(v[0], e);
+      }
     }
   }
-}
 
-template <typename T, int D>
-__device__ inline void store_tile(PrefillTileLds<D>& s, const TileRegs<D>& r) {
+  template <typename T>
+  __device__ inline void store_tile(PrefillTileLds<D>& s) const {
 #pragma unroll
-  for (int u = 0; u < TileRegs<D>::kKChunks; ++u) store_k_chunk<T, D>(s, r, u);
-  store_v<T, D>(s, r);
-}
+    for (int u = 0; u < kKChunks; ++u) store_k_chunk<T>(s, u);
+    store_v<T>(s);
+  }
+};
 
 // S^T for the 32 keys of block kb of an LDS tile against this wave's 32
 // queries.  All K fragments are read before the first MFMA (the scheduler is
@@ -297,7 +312,7 @@ void prefill_mfma_kernel(PrefillArgs a) {
   if (qt * kBM >= S_b) return;
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int j = lane & 31;          // query of this lane within the wave's 32
   const int hh = lane >> 5;         // lane half
   const int kvh = h / (a.H / a.Hkv);
@@ -347,16 +362,17 @@ void prefill_mfma_kernel(PrefillArgs a) {
   // While tile kt is consumed from one buffer, tile kt+1 (loaded during
   // iteration kt-1) is written into the other, and tile kt+2 is loaded;
   // tile kt+3's block ids are fetched at the end of the tile.
+  using P = Producer<D>;
   const int n_kt = kend > 0 ? (kend + kBN - 1) / kBN : 0;
-  TileRegs<D> regs;
-  TileIds<D> ids;
+  P pr;
+  pr.init(a, wave, kvh);
   if (n_kt > 0) {
-    tile_ids<D>(a, ids, bt, 0);
-    load_tile<T, D>(a, regs, ids, kvh);
-    if (n_kt > 1) tile_ids<D>(a, ids, bt, 1);
-    store_tile<T, D>(lds[0], regs);
-    if (n_kt > 1) load_tile<T, D>(a, regs, ids, kvh);
-    if (n_kt > 2) tile_ids<D>(a, ids, bt, 2);
+    pr.fetch_ids(a, bt, 0);
+    pr.template load_tile<T>(a);
+    if (n_kt > 1) pr.fetch_ids(a, bt, 1);
+    pr.template store_tile<T>(lds[0]);
+    if (n_kt > 1) pr.template load_tile<T>(a);
+    if (n_kt > 2) pr.fetch_ids(a, bt, 2);
     __syncthreads();
   }
 
@@ -366,40 +382,33 @@ void prefill_mfma_kernel(PrefillArgs a) {
     const bool fetch = kt + 2 < n_kt;       // tile kt+2's loads go out now
     const PrefillTileLds<D>& t = lds[cur];
     const int tile_key0 = kt * kBN;
-    // 32-key blocks of this tile that reach this wave's rows
+    // 32-key blocks of this tile that reach this wave's rows (wave-uniform)
     const int nkb = w_lim_max < tile_key0 ? 0 : min(kNKB, (w_lim_max - tile_key0) / 32 + 1);
-
-    // Software pipeline: the MFMAs of block kb+1's scores are issued before
-    // block kb's softmax, so they run while the VALU works on the softmax.
-    float16x s_cur;
-    if (nkb > 0) s_cur = qk_block<D>(t, 0, qf, j, hh);
 
 #pragma unroll
     for (int kb = 0; kb < kNKB; ++kb) {
       // Producer share of this block: write part of tile kt+1 into the idle
-      // buffer (V at block 0, K chunks spread over the blocks) and re-use the freed
-      // registers for the matching loads of tile kt+2, which then have a
-      // whole tile of compute to arrive.
+      // buffer (V at block 0, K chunks spread over the blocks) and re-use the
+      // freed registers for the matching loads of tile kt+2, which then have
+      // a whole tile of compute to arrive.
       if (fill) {
         if (kb == 0) {
-          store_v<T, D>(lds[cur ^ 1], regs);
-          if (fetch) load_v<T, D>(a, regs, ids, kvh);
+          pr.template store_v<T>(lds[cur ^ 1]);
+          if (fetch) pr.template load_v<T>(a);
         }
 #pragma unroll
-        for (int cc = 0; cc < TileRegs<D>::kChunksPerBlock; ++cc) {
-          const int u = kb * TileRegs<D>::kChunksPerBlock + cc;
-          if (u < TileRegs<D>::kKChunks) {
-            store_k_chunk<T, D>(lds[cur ^ 1], regs, u);
-            if (fetch) load_k_chunk<T, D>(a, regs, ids, kvh, u);
+        for (int cc = 0; cc < P::kChunksPerBlock; ++cc) {
+          const int u = kb * P::kChunksPerBlock + cc;
+          if (u < P::kKChunks) {
+            pr.template store_k_chunk<T>(lds[cur ^ 1], u);
+            if (fetch) pr.template load_k_chunk<T>(a, u);
           }
         }
       }
-      if (kb == kNKB - 1 && fetch && kt + 3 < n_kt) tile_ids<D>(a, ids, bt, kt + 3);
+      if (kb == kNKB - 1 && fetch && kt + 3 < n_kt) pr.fetch_ids(a, bt, kt + 3);
       if (kb >= nkb) continue;
 
-      const bool more = kb + 1 < nkb;
-      float16x s_next;
-      if (more) s_next = qk_block<D>(t, kb + 1, qf, j, hh);
+      float16x s = qk_block<D>(t, kb, qf, j, hh);
 
       // V^T fragments of this block, read before the softmax so that their
       // latency hides behind it.
@@ -416,14 +425,14 @@ void prefill_mfma_kernel(PrefillArgs a) {
       if (key0 + 31 > w_lim_min) {
 #pragma unroll
         for (int r = 0; r < 16; ++r)
-          if (key0 + 16 * (r >> 3) + 8 * hh + (r & 7) > lim) s_cur[r] = -INFINITY;
+          if (key0 + 16 * (r >> 3) + 8 * hh + (r & 7) > lim) s[r] = -INFINITY;
       }
 
       // online softmax; the max is only raised when it grows by > 8
-      float mx = kNegBig;
+      float mx = s[0];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s_cur[r]);
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[r]);
+      mx = max_halves(mx);
       if (__builtin_amdgcn_ballot_w64(mx > m + kRescaleSlack) != 0) {
         const float m_new = fmaxf(m, mx);
         const float corr = fast_exp2(m - m_new);
@@ -441,8 +450,7 @@ void prefill_mfma_kernel(PrefillArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           // masked scores are -inf: exp2(-inf) = 0
-          w[i] = pack_f16(fast_exp2(s_cur[8 * hf + 2 * i] - m),
-                          fast_exp2(s_cur[8 * hf + 2 * i + 1] - m));
+          w[i] = pack_f16(fast_exp2(s[8 * hf + 2 * i] - m), fast_exp2(s[8 * hf + 2 * i + 1] - m));
           // the row sum adds the fp16 probabilities P.V will use
           l = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2x, w[i]),
                                      (half2x){(_Float16)1.0f, (_Float16)1.0f}, l, false);
@@ -456,15 +464,13 @@ void prefill_mfma_kernel(PrefillArgs a) {
 #pragma unroll
         for (int d = 0; d < kDB; ++d)
           o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[kc][d], p[kc], o[d], 0, 0, 0);
-
-      if (more) s_cur = s_next;
     }
     __syncthreads();   // the idle buffer is complete; this tile is consumed
   }
 
   // ---- normalise and store: lane (j, hh) owns query j and dims
   // d*32 + 8*g + 4*hh + (0..3) ----
-  const float lsum = l + __shfl_xor(l, 32);
+  const float lsum = sum_halves(l);
   if (!row_ok) return;
   const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
   float* op = a.out + ((int64_t)(row0 + i_row) * a.H + h) * D + 4 * hh;
