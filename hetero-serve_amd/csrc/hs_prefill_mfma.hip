@@ -50,6 +50,8 @@
 // through that XCD's L2.
 #include "hs_kernels.h"
 
+#include <type_traits>
+
 namespace hs {
 
 namespace {
@@ -166,9 +168,7 @@ __device__ inline float max_halves(float x) {
 //      8*(tid / (64/kG)), so that its transposed LDS store for one dim is one
 //      kG*2-byte write and 64/kG neighbouring lanes fill one V^T row segment.
 //      Its kG keys lie in one page: one block id and one base per tile.
-// The four block ids of a tile are fetched by one vector load (lane L reads
-// the id of the page its V keys are in); K page p's id is read from the lane
-// that holds it.
+// The block ids of a tile are fetched by one vector load, a tile ahead.
 template <int D>
 struct Producer {
   static constexpr int kDC = D / 8;                         // 16-byte chunks per head row
@@ -181,9 +181,13 @@ struct Producer {
   static_assert(kKeysPerU % 16 == 0 && 16 % kG == 0, "loads must not straddle pages");
   static constexpr int kChunksPerBlock = (kKChunks + kBN / 32 - 1) / (kBN / 32);
 
-  uint4 k[kKChunks];   // tile in flight
-  uint4 v[kG];
-  int id;              // block id of page (this lane's V page) of the tile being fetched
+  // One tile in flight from global memory.
+  struct Regs {
+    uint4 k[kKChunks];
+    uint4 v[kG];
+  };
+
+  int vid[2];          // block id of this lane's V page for tiles of parity 0 / 1
 
   // per-thread constants
   uint32_t koff;       // byte offset of this lane's K chunk inside a page (+ head)
@@ -203,44 +207,49 @@ struct Producer {
     voff = (key0 % 16) * tok + kvh * D + (tid / kGroups) * 8;
   }
 
+  // One vector load per tile: lane L reads the id of the page its V keys are
+  // in; K page p's id is read from a lane that holds it.  Tile t's id lives
+  // in slot t % 2 and is fetched before the loads of the tile before it, so
+  // waiting for it never waits for a K/V load issued later.
+  template <int kSlot>
   __device__ inline void fetch_ids(const PrefillArgs& a, const int32_t* bt, int kt) {
-    id = bt[min(kt * kPages + vpage, a.MB - 1)];
+    vid[kSlot] = bt[min(kt * kPages + vpage, a.MB - 1)];
   }
 
-  template <typename T>
-  __device__ inline void load_k_chunk(const PrefillArgs& a, int u) {
+  template <typename T, int kSlot>
+  __device__ inline void load_k_chunk(const PrefillArgs& a, Regs& r, int u) const {
     const int page = kpage0 + u * (kKeysPerU / 16);              // wave-uniform
-    const int kid = __builtin_amdgcn_readlane(id, page * 16 / kG);
+    const int kid = __builtin_amdgcn_readlane(vid[kSlot], page * 16 / kG);
     const char* base = reinterpret_cast<const char*>(a.k) +
                        safe_block(kid, a.NB) * tok * 16 * (int64_t)sizeof(T);
-    k[u] = load16(base + koff);
+    r.k[u] = load16(base + koff);
   }
 
-  template <typename T>
-  __device__ inline void load_v(const PrefillArgs& a) {
-    const T* p = reinterpret_cast<const T*>(a.v) + safe_block(id, a.NB) * tok * 16 + voff;
+  template <typename T, int kSlot>
+  __device__ inline void load_v(const PrefillArgs& a, Regs& r) const {
+    const T* p = reinterpret_cast<const T*>(a.v) + safe_block(vid[kSlot], a.NB) * tok * 16 + voff;
 #pragma unroll
-    for (int g = 0; g < kG; ++g) v[g] = load16(p + g * tok);
+    for (int g = 0; g < kG; ++g) r.v[g] = load16(p + g * tok);
   }
 
-  template <typename T>
-  __device__ inline void load_tile(const PrefillArgs& a) {
+  template <typename T, int kSlot>
+  __device__ inline void load_tile(const PrefillArgs& a, Regs& r) const {
 #pragma unroll
-    for (int u = 0; u < kKChunks; ++u) load_k_chunk<T>(a, u);
-    load_v<T>(a);
+    for (int u = 0; u < kKChunks; ++u) load_k_chunk<T, kSlot>(a, r, u);
+    load_v<T, kSlot>(a, r);
   }
 
   // Registers -> LDS (fp16; K with the bit-2/3 row swap, V transposed).
   template <typename T>
-  __device__ inline void store_k_chunk(PrefillTileLds<D>& s, int u) const {
+  __device__ inline void store_k_chunk(PrefillTileLds<D>& s, const Regs& r, int u) const {
     const int t_k = threadIdx.x / kDC;
     const int row0 = (t_k & ~31) | swap_bits23(t_k & 31);
     *reinterpret_cast<uint4*>(&s.k[row0 + u * kKeysPerU][(threadIdx.x % kDC) * 8]) =
-        to_f16x8<T>(k[u]);
+        to_f16x8<T>(r.k[u]);
   }
 
   template <typename T>
-  __device__ inline void store_v(PrefillTileLds<D>& s) const {
+  __device__ inline void store_v(PrefillTileLds<D>& s, const Regs& r) const {
     const int key0 = kG * (threadIdx.x % kGroups);
     const int dc = threadIdx.x / kGroups;
 #pragma unroll
@@ -248,20 +257,20 @@ struct Producer {
       _Float16* dst = &s.vt[dc * 8 + e][key0];
       if constexpr (kG == 4) {
         *reinterpret_cast<uint2*>(dst) =
-            make_uint2(pack_col<T>(v[0], v[1], e), pack_col<T>(v[2], v[3], e));
+            make_uint2(pack_col<T>(r.v[0], r.v[1], e), pack_col<T>(r.v[2], r.v[3], e));
       } else if constexpr (kG == 2) {
-        *reinterpret_cast<uint32_t*>(dst) = pack_col<T>(v[0], v[1], e);
+        *reinterpret_cast<uint32_t*>(dst) = pack_col<T>(r.v[0], r.v[1], e);
       } else {
-        *dst = (_Float16)elem_f32<T>(v[0], e);
+        *dst = (_Float16)elem_f32<T>(r.v[0], e);
       }
     }
   }
 
   template <typename T>
-  __device__ inline void store_tile(PrefillTileLds<D>& s) const {
+  __device__ inline void store_tile(PrefillTileLds<D>& s, const Regs& r) const {
 #pragma unroll
-    for (int u = 0; u < kKChunks; ++u) store_k_chunk<T>(s, u);
-    store_v<T>(s);
+    for (int u = 0; u < kKChunks; ++u) store_k_chunk<T>(s, r, u);
+    store_v<T>(s, r);
   }
 };
 
@@ -359,53 +368,62 @@ void prefill_mfma_kernel(PrefillArgs a) {
   float l = 0.0f;      // this lane's share of the running sum
 
   // ---- key tiles: double-buffered LDS, one barrier per tile ---------------
-  // While tile kt is consumed from one buffer, tile kt+1 (loaded during
-  // iteration kt-1) is written into the other, and tile kt+2 is loaded;
-  // tile kt+3's block ids are fetched at the end of the tile.
+  // Tiles pass through two register sets (tile t in set t % 2) and two LDS
+  // buffers (tile t in buffer t % 2).  While tile kt is consumed from LDS,
+  // tile kt+1 is written from its register set into the idle buffer and that
+  // set is refilled with tile kt+3, so a load has two tiles of compute to
+  // arrive.  Block ids run one tile ahead of the loads.
   using P = Producer<D>;
   const int n_kt = kend > 0 ? (kend + kBN - 1) / kBN : 0;
   P pr;
   pr.init(a, wave, kvh);
+  typename P::Regs rs[2];
+  // Every load and block-id fetch below is unconditional (ids are clamped to
+  // the table, and a tile past the end re-reads a valid page), so that the
+  // compiler can count outstanding loads exactly and wait only for the tile
+  // it is about to store: a load issued under a condition makes it wait for
+  // all of them.
   if (n_kt > 0) {
-    pr.fetch_ids(a, bt, 0);
-    pr.template load_tile<T>(a);
-    if (n_kt > 1) pr.fetch_ids(a, bt, 1);
-    pr.template store_tile<T>(lds[0]);
-    if (n_kt > 1) pr.template load_tile<T>(a);
-    if (n_kt > 2) pr.fetch_ids(a, bt, 2);
+    pr.template fetch_ids<0>(a, bt, 0);
+    pr.template fetch_ids<1>(a, bt, 1);
+    pr.template load_tile<T, 0>(a, rs[0]);
+    pr.template load_tile<T, 1>(a, rs[1]);
+    pr.template fetch_ids<0>(a, bt, 2);
+    pr.template store_tile<T>(lds[0], rs[0]);
+    pr.template load_tile<T, 0>(a, rs[0]);
+    pr.template fetch_ids<1>(a, bt, 3);
     __syncthreads();
   }
 
-  for (int kt = 0; kt < n_kt; ++kt) {
-    const int cur = kt & 1;
-    const bool fill = kt + 1 < n_kt;        // tile kt+1 sits in registers
-    const bool fetch = kt + 2 < n_kt;       // tile kt+2's loads go out now
-    const PrefillTileLds<D>& t = lds[cur];
+  // One tile: consume tile kt from buffer kSet ^ 1, write tile kt+1 from
+  // register set kSet into buffer kSet, refill set kSet with tile kt+3.
+  auto tile_step = [&](auto set_tag, int kt) {
+    constexpr int kSet = decltype(set_tag)::value;
+    typename P::Regs& r = rs[kSet];
+    PrefillTileLds<D>& nxt = lds[kSet];
+    const PrefillTileLds<D>& t = lds[kSet ^ 1];
+    const bool fill = kt + 1 < n_kt;        // tile kt+1 sits in set kSet
     const int tile_key0 = kt * kBN;
     // 32-key blocks of this tile that reach this wave's rows (wave-uniform)
     const int nkb = w_lim_max < tile_key0 ? 0 : min(kNKB, (w_lim_max - tile_key0) / 32 + 1);
 
 #pragma unroll
     for (int kb = 0; kb < kNKB; ++kb) {
-      // Producer share of this block: write part of tile kt+1 into the idle
-      // buffer (V at block 0, K chunks spread over the blocks) and re-use the
-      // freed registers for the matching loads of tile kt+2, which then have
-      // a whole tile of compute to arrive.
-      if (fill) {
-        if (kb == 0) {
-          pr.template store_v<T>(lds[cur ^ 1]);
-          if (fetch) pr.template load_v<T>(a);
-        }
+      // Producer share of this block: V at block 0, K chunks spread over the
+      // blocks; each store frees registers for the matching load of tile kt+3.
+      if (kb == 0) {
+        pr.template fetch_ids<kSet ^ 1>(a, bt, kt + 4);   // slot of tile kt+4
+        if (fill) pr.template store_v<T>(nxt, r);
+        pr.template load_v<T, kSet>(a, r);                // tile kt+3
+      }
 #pragma unroll
-        for (int cc = 0; cc < P::kChunksPerBlock; ++cc) {
-          const int u = kb * P::kChunksPerBlock + cc;
-          if (u < P::kKChunks) {
-            pr.template store_k_chunk<T>(lds[cur ^ 1], u);
-            if (fetch) pr.template load_k_chunk<T>(a, u);
-          }
+      for (int cc = 0; cc < P::kChunksPerBlock; ++cc) {
+        const int u = kb * P::kChunksPerBlock + cc;
+        if (u < P::kKChunks) {
+          if (fill) pr.template store_k_chunk<T>(nxt, r, u);
+          pr.template load_k_chunk<T, kSet>(a, r, u);
         }
       }
-      if (kb == kNKB - 1 && fetch && kt + 3 < n_kt) pr.fetch_ids(a, bt, kt + 3);
       if (kb >= nkb) continue;
 
       float16x s = qk_block<D>(t, kb, qf, j, hh);
@@ -465,7 +483,14 @@ void prefill_mfma_kernel(PrefillArgs a) {
         for (int d = 0; d < kDB; ++d)
           o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[kc][d], p[kc], o[d], 0, 0, 0);
     }
-    __syncthreads();   // the idle buffer is complete; this tile is consumed
+    __syncthreads();   // buffer kSet is complete; buffer kSet ^ 1 is consumed
+  };
+
+  // An odd count runs one empty step (nothing consumed or stored) so that
+  // both steps of a pair are unconditional.
+  for (int kt = 0; kt < n_kt; kt += 2) {
+    tile_step(std::integral_constant<int, 1>{}, kt);
+    tile_step(std::integral_constant<int, 0>{}, kt + 1);
   }
 
   // ---- normalise and store: lane (j, hh) owns query j and dims
