@@ -378,11 +378,12 @@ void prefill_mfma_kernel(PrefillArgs a) {
   P pr;
   pr.init(a, wave, kvh);
   typename P::Regs rs[2];
-  // Every load and block-id fetch below is unconditional (ids are clamped to
-  // the table, and a tile past the end re-reads a valid page), so that the
-  // compiler can count outstanding loads exactly and wait only for the tile
-  // it is about to store: a load issued under a condition makes it wait for
-  // all of them.
+  // In the main loop every load and block-id fetch is unconditional, so that
+  // the compiler counts outstanding loads exactly and waits only for the tile
+  // it is about to store (a load issued under a condition makes it wait for
+  // all of them).  The last tile pairs run a tail copy of the step that loads
+  // only what is still needed.  The prologue's loads are unconditional too:
+  // ids are clamped to the table and a tile past the end reads a valid page.
   if (n_kt > 0) {
     pr.template fetch_ids<0>(a, bt, 0);
     pr.template fetch_ids<1>(a, bt, 1);
@@ -397,8 +398,10 @@ void prefill_mfma_kernel(PrefillArgs a) {
 
   // One tile: consume tile kt from buffer kSet ^ 1, write tile kt+1 from
   // register set kSet into buffer kSet, refill set kSet with tile kt+3.
-  auto tile_step = [&](auto set_tag, int kt) {
+  auto tile_step = [&](auto set_tag, auto main_tag, int kt) {
     constexpr int kSet = decltype(set_tag)::value;
+    constexpr bool kMain = decltype(main_tag)::value;   // loads known to be needed
+    const bool load = kMain || kt + 3 < n_kt;
     typename P::Regs& r = rs[kSet];
     PrefillTileLds<D>& nxt = lds[kSet];
     const PrefillTileLds<D>& t = lds[kSet ^ 1];
@@ -412,16 +415,16 @@ void prefill_mfma_kernel(PrefillArgs a) {
       // Producer share of this block: V at block 0, K chunks spread over the
       // blocks; each store frees registers for the matching load of tile kt+3.
       if (kb == 0) {
-        pr.template fetch_ids<kSet ^ 1>(a, bt, kt + 4);   // slot of tile kt+4
+        if (kMain || kt + 4 < n_kt) pr.template fetch_ids<kSet ^ 1>(a, bt, kt + 4);
         if (fill) pr.template store_v<T>(nxt, r);
-        pr.template load_v<T, kSet>(a, r);                // tile kt+3
+        if (load) pr.template load_v<T, kSet>(a, r);      // tile kt+3
       }
 #pragma unroll
       for (int cc = 0; cc < P::kChunksPerBlock; ++cc) {
         const int u = kb * P::kChunksPerBlock + cc;
         if (u < P::kKChunks) {
           if (fill) pr.template store_k_chunk<T>(nxt, r, u);
-          pr.template load_k_chunk<T, kSet>(a, r, u);
+          if (load) pr.template load_k_chunk<T, kSet>(a, r, u);
         }
       }
       if (kb >= nkb) continue;
@@ -486,11 +489,20 @@ void prefill_mfma_kernel(PrefillArgs a) {
     __syncthreads();   // buffer kSet is complete; buffer kSet ^ 1 is consumed
   };
 
-  // An odd count runs one empty step (nothing consumed or stored) so that
-  // both steps of a pair are unconditional.
-  for (int kt = 0; kt < n_kt; kt += 2) {
-    tile_step(std::integral_constant<int, 1>{}, kt);
-    tile_step(std::integral_constant<int, 0>{}, kt + 1);
+  // Pairs of steps (so that register sets and LDS buffers are static); an
+  // odd count ends with one empty step (nothing consumed or stored).
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+  using Main = std::true_type;
+  using Tail = std::false_type;
+  int kt = 0;
+  for (; kt + 4 < n_kt; kt += 2) {
+    tile_step(S1{}, Main{}, kt);
+    tile_step(S0{}, Main{}, kt + 1);
+  }
+  for (; kt < n_kt; kt += 2) {
+    tile_step(S1{}, Tail{}, kt);
+    tile_step(S0{}, Tail{}, kt + 1);
   }
 
   // ---- normalise and store: lane (j, hh) owns query j and dims
