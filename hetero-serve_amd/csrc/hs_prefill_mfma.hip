@@ -70,6 +70,7 @@ constexpr int kXcds = 8;
 constexpr int kKPad = 8;                     // halves of padding per LDS K row
 constexpr int kVPad = 8;                     // halves of padding per LDS V^T row
 constexpr float kRescaleSlack = 8.0f;        // log2 units
+constexpr int kMaxRanked = 256;              // query tiles a workgroup ranks itself
 
 struct PrefillArgs {
   const float* q;        // [rows, H, D]
@@ -82,6 +83,7 @@ struct PrefillArgs {
   int S, B, H, Hkv, MB, NB;
   int n_qt;              // query tiles per (sequence, head) in the grid
   int slots_per_xcd;     // grid = kXcds * slots_per_xcd
+  int ranked;            // 1: query tiles are dispatched longest first (B * n_qt <= kMaxRanked)
   float qscale;          // scale * log2(e)
 };
 
@@ -294,6 +296,67 @@ __device__ inline float16x qk_block(const PrefillTileLds<D>& t, int kb, const ha
   return s;
 }
 
+// Longest-first dispatch.  Every workgroup ranks the batch's sequences by the
+// keys their last (heaviest) query tile walks, descending, and lays out the
+// query tiles sequence by sequence in that order, each sequence's tiles
+// heaviest first; the workgroup takes the tile of rank `slot / nh` for its
+// slot.  Head h runs on XCD h % 8, so the query tiles of one (sequence, head)
+// run close together on one XCD and share its L2, and each XCD gets the same
+// mix of work.  Ranking sequences rather than single tiles keeps that
+// sharing: tiles of equal length from different sequences would otherwise
+// interleave and evict each other's K/V.  Returns false when the slot has no
+// tile.
+struct RankScratch {
+  int keys[kMaxRanked];      // keys walked by each sequence's last tile
+  int order[kMaxRanked];     // sequences by decreasing keys
+  int b, qt;
+};
+
+__device__ inline int seq_rows(const PrefillArgs& a, int b) {
+  return a.cu_q ? a.cu_q[b + 1] - a.cu_q[b] : a.S;
+}
+
+__device__ inline bool ranked_tile(const PrefillArgs& a, RankScratch& rs, int& b, int& h, int& qt) {
+  const int xcd = blockIdx.x % kXcds;
+  const int slot = blockIdx.x / kXcds;
+  const int nh = a.H > xcd ? (a.H - xcd + kXcds - 1) / kXcds : 0;   // heads on this XCD
+  if (nh == 0) return false;
+  const int r = slot / nh;
+  const int tid = threadIdx.x;
+  if (tid < a.B) rs.keys[tid] = seq_rows(a, tid) > 0 ? min(a.MB * 16, a.ctx[tid]) : -1;
+  if (tid == 0) rs.b = -1;
+  __syncthreads();
+  if (tid < a.B) {
+    const int k = rs.keys[tid];
+    int rank = 0;
+    for (int q = 0; q < a.B; ++q) {
+      const int kq = rs.keys[q];
+      rank += (kq > k) | ((kq == k) & (q < tid));
+    }
+    rs.order[rank] = tid;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int start = 0;
+    for (int i = 0; i < a.B; ++i) {
+      const int bb = rs.order[i];
+      const int n = (seq_rows(a, bb) + kBM - 1) / kBM;
+      if (r < start + n) {
+        rs.b = bb;
+        rs.qt = n - 1 - (r - start);
+        break;
+      }
+      start += n;
+    }
+  }
+  __syncthreads();
+  b = rs.b;
+  if (b < 0) return false;
+  qt = rs.qt;
+  h = xcd + kXcds * (slot % nh);
+  return true;
+}
+
 template <typename T, int D>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 void prefill_mfma_kernel(PrefillArgs a) {
@@ -303,13 +366,20 @@ void prefill_mfma_kernel(PrefillArgs a) {
   __shared__ PrefillTileLds<D> lds[2];
 
   // ---- which (sequence, head, query tile) -------------------------------
-  const int xcd = blockIdx.x % kXcds;
-  const int slot = blockIdx.x / kXcds;
-  const int pair = (slot / a.n_qt) * kXcds + xcd;     // (b * H + h)
-  if (pair >= a.B * a.H) return;
-  const int qt = a.n_qt - 1 - slot % a.n_qt;          // heaviest tile first
-  const int b = pair / a.H;
-  const int h = pair - b * a.H;
+  int b, h, qt;
+  if (a.ranked) {
+    __shared__ RankScratch rank_scratch;
+    if (!ranked_tile(a, rank_scratch, b, h, qt)) return;
+  } else {
+    // all query tiles of one (sequence, head) on one XCD, heaviest first
+    const int xcd = blockIdx.x % kXcds;
+    const int slot = blockIdx.x / kXcds;
+    const int pair = (slot / a.n_qt) * kXcds + xcd;     // (b * H + h)
+    if (pair >= a.B * a.H) return;
+    qt = a.n_qt - 1 - slot % a.n_qt;
+    b = pair / a.H;
+    h = pair - b * a.H;
+  }
   int row0, S_b;
   if (a.cu_q) {
     row0 = a.cu_q[b];
@@ -561,7 +631,9 @@ int launch_prefill_mfma(const float* q, const int32_t* cu_q, int S, int max_rows
   a.NB = NB;
   a.n_qt = (max_rows_per_seq + kBM - 1) / kBM;
   const int64_t pairs = (int64_t)B * H;
-  const int64_t slots = (pairs + kXcds - 1) / kXcds * a.n_qt;
+  a.ranked = (int64_t)B * a.n_qt <= kMaxRanked;
+  const int64_t slots = a.ranked ? (int64_t)B * a.n_qt * ((H + kXcds - 1) / kXcds)
+                                 : (pairs + kXcds - 1) / kXcds * a.n_qt;
   if (slots * kXcds > 0x7fffffffLL) return fail(HS_EUNSUPPORTED, "prefill grid too large");
   a.slots_per_xcd = (int)slots;
   a.qscale = scale * kLog2e;
