@@ -285,7 +285,9 @@ def main() -> int:
     if not args.no_secondary:
         try:
             pc = cases.c4_prefill(dev)
-            pre = prefill_leg(pc, max(5, args.steps // 5), 2)
+            # >= 60 warm-up launches (~20 ms): after the memory-bound decode leg
+            # the clock takes tens of milliseconds of MFMA work to ramp up
+            pre = prefill_leg(pc, max(20, args.steps // 5), max(60, args.warmup))
             secondary["C4_prefill"] = {
                 "us_per_step": round(pre["step_ms"] * 1e3, 2),
                 "tflops": round(pre["step_tflops"], 2),
