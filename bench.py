@@ -173,6 +173,71 @@ def pack_leg(steps: int, warmup: int) -> dict:
                 kernel_gbs=nbytes / (k_ms * 1e-3) / 1e9, step_gbs=nbytes / (step_ms * 1e-3) / 1e9)
 
 
+def kv_write_leg(steps: int, warmup: int) -> dict:
+    """C5's prefill chunk written into the cache: 1024 tokens at positions
+    2048..3071 of one sequence, K and V as strided fp32 slices of a fused QKV
+    output [1024, 3 * 4096], cast into a bf16 layer cache (the engine's step at
+    torch_engine.py:294-308).  Checked bit for bit against the reference's own
+    ``fk[slots] = k.to(dtype)`` on the same GPU, which is also timed."""
+    import torch
+
+    from heteroserve import _hip
+    from hsbench.timing import Event, time_steps
+
+    lib = _hip.lib()
+    dev = "cuda:0"
+    nb, bs, h, d, T, start = 8192, 16, 32, 128, 1024, 2048
+    g = torch.Generator(device=dev).manual_seed(43)
+    kc = torch.zeros((nb, bs, h, d), dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros_like(kc)
+    table = torch.randperm(nb, generator=g, device=dev)[: (start + T) // bs].to(torch.int32)
+    bt = table.view(1, -1).contiguous()
+    pos = torch.arange(start, start + T, dtype=torch.int32, device=dev)
+    seq = torch.zeros(T, dtype=torch.int32, device=dev)
+    kvd = h * d
+    qkv = torch.randn((T, 3 * kvd), generator=g, device=dev)
+    k, v = qkv[:, kvd:2 * kvd], qkv[:, 2 * kvd:]
+    stream = torch.cuda.current_stream().cuda_stream
+    args = (kc.data_ptr(), vc.data_ptr(), _hip.dtype_code(kc.dtype), nb, bs, h, d, bt.data_ptr(),
+            bt.shape[1], pos.data_ptr(), seq.data_ptr(), T, k.data_ptr(), v.data_ptr(),
+            _hip.DTYPE_F32, qkv.stride(0), stream)
+
+    def step():
+        _hip.check(lib.hs_kv_append(*args))
+
+    def arm(s_, e_):
+        _hip.check(lib.hs_profile_next_launch(s_.handle, e_.handle))
+
+    step_ms, kernel_ms, _ = time_steps(step, steps, warmup, stream, arm)
+    # the reference's code path on the same device: slots_for + index_put
+    slots = (table.long()[pos.long() // bs] * bs + pos.long() % bs)
+    fk, fv = kc.clone().view(nb * bs, h, d), vc.clone().view(nb * bs, h, d)
+    fk.zero_()
+    fv.zero_()
+
+    def ref_step():
+        fk[slots] = k.view(T, h, d).to(kc.dtype)
+        fv[slots] = v.view(T, h, d).to(vc.dtype)
+
+    for _ in range(warmup):
+        ref_step()
+    e0, e1 = Event(), Event()
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(steps):
+        ref_step()
+    e1.record(stream)
+    ref_ms = e0.elapsed_ms(e1) / steps
+    exact = bool(torch.equal(fk.view(torch.int16), kc.view(nb * bs, h, d).view(torch.int16)) and
+                 torch.equal(fv.view(torch.int16), vc.view(nb * bs, h, d).view(torch.int16)))
+    nbytes = 2 * T * kvd * (4 + 2)        # read fp32 rows, write bf16 rows, K and V
+    k_ms = statistics.mean(kernel_ms)
+    del kc, vc, fk, fv, qkv
+    torch.cuda.empty_cache()
+    return dict(step_ms=step_ms, kernel_ms=k_ms, ref_ms=ref_ms, bytes=nbytes, bit_exact=exact,
+                kernel_gbs=nbytes / (k_ms * 1e-3) / 1e9)
+
+
 # ---------------------------------------------------------------------------
 # CPU baseline: the oracle on this host's cores
 # ---------------------------------------------------------------------------
@@ -308,6 +373,15 @@ def main() -> int:
         }
         log(f"C5 pack: {pk['kernel_ms'] * 1e3:.1f} us, {pk['kernel_gbs']:.0f} GB/s, "
             f"exact={pk['bit_exact']}")
+        kw = kv_write_leg(max(20, args.steps // 5), 10)
+        secondary["C5_kv_write"] = {
+            "us_per_step": round(kw["step_ms"] * 1e3, 2), "gbs": round(kw["kernel_gbs"], 1),
+            "hbm_frac": round(kw["kernel_gbs"] / HBM_PEAK_GBS, 4), "bit_exact": kw["bit_exact"],
+            "bytes_moved": kw["bytes"], "torch_index_put_us": round(kw["ref_ms"] * 1e3, 2),
+        }
+        log(f"C5 KV write (1024-token chunk): {kw['kernel_ms'] * 1e3:.1f} us, "
+            f"{kw['kernel_gbs']:.0f} GB/s, torch fk[slots]=k: {kw['ref_ms'] * 1e3:.1f} us, "
+            f"exact={kw['bit_exact']}")
 
     line = {
         "metric": METRIC,

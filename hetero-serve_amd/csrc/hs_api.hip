@@ -306,4 +306,46 @@ int hs_kv_gather(const void* cache, int NB, int BS, int64_t row_bytes, const int
                             static_cast<hipStream_t>(stream));
 }
 
+static int check_kv_write(void* k_cache, void* v_cache, int kv_dtype, int Hkv, int D,
+                          int64_t n, const void* k_src, const void* v_src, int src_dtype,
+                          int64_t src_row_stride) {
+  if (n < 0 || Hkv <= 0 || D <= 0) return fail(HS_EINVAL, "KV write sizes must be positive");
+  if (kv_dtype < HS_DTYPE_F32 || kv_dtype > HS_DTYPE_BF16 || src_dtype < HS_DTYPE_F32 ||
+      src_dtype > HS_DTYPE_BF16)
+    return fail(HS_EINVAL, "unsupported dtype code");
+  if (src_row_stride < (int64_t)Hkv * D)
+    return fail(HS_EINVAL, "source row stride is smaller than Hkv * D");
+  if (n > 0 && (!k_cache || !v_cache || !k_src || !v_src)) return fail(HS_EINVAL, "null pointer");
+  return HS_OK;
+}
+
+int hs_kv_scatter(void* k_cache, void* v_cache, int kv_dtype, int64_t num_slots, int Hkv, int D,
+                  const int64_t* slots, int64_t n, const void* k_src, const void* v_src,
+                  int src_dtype, int64_t src_row_stride, void* stream) {
+  const int rc = check_kv_write(k_cache, v_cache, kv_dtype, Hkv, D, n, k_src, v_src, src_dtype,
+                                src_row_stride);
+  if (rc != HS_OK) return rc;
+  if (num_slots <= 0) return fail(HS_EINVAL, "num_slots must be positive");
+  if (n == 0) return HS_OK;
+  if (!slots) return fail(HS_EINVAL, "null pointer");
+  return launch_kv_scatter(k_cache, v_cache, kv_dtype, num_slots, (int64_t)Hkv * D, slots, n,
+                           k_src, v_src, src_dtype, src_row_stride,
+                           static_cast<hipStream_t>(stream));
+}
+
+int hs_kv_append(void* k_cache, void* v_cache, int kv_dtype, int NB, int BS, int Hkv, int D,
+                 const int32_t* block_tables, int MB, const int32_t* positions,
+                 const int32_t* seq_ids, int64_t n, const void* k_src, const void* v_src,
+                 int src_dtype, int64_t src_row_stride, void* stream) {
+  const int rc = check_kv_write(k_cache, v_cache, kv_dtype, Hkv, D, n, k_src, v_src, src_dtype,
+                                src_row_stride);
+  if (rc != HS_OK) return rc;
+  if (NB <= 0 || BS <= 0 || MB <= 0) return fail(HS_EINVAL, "append sizes must be positive");
+  if (n == 0) return HS_OK;
+  if (!block_tables || !positions) return fail(HS_EINVAL, "null pointer");
+  return launch_kv_append(k_cache, v_cache, kv_dtype, NB, BS, (int64_t)Hkv * D, block_tables, MB,
+                          positions, seq_ids, n, k_src, v_src, src_dtype, src_row_stride,
+                          static_cast<hipStream_t>(stream));
+}
+
 }  // extern "C"

@@ -41,6 +41,16 @@ int launch_page_copy(const void* pool, void* buf, bool unpack, int L, int NB, in
 int launch_gather_rows(const void* cache, int NB, int BS, int64_t row_bytes, const int32_t* bt,
                        int MB, int B, int length, void* out, hipStream_t stream);
 
+// New K/V rows into the cache (hs_kvwrite.hip): rows of row_elems elements,
+// source rows src_row_stride elements apart, cast to the cache dtype.
+int launch_kv_scatter(void* k_cache, void* v_cache, int kv_dtype, int64_t num_slots,
+                      int64_t row_elems, const int64_t* slots, int64_t n, const void* k_src,
+                      const void* v_src, int src_dtype, int64_t src_row_stride, hipStream_t stream);
+int launch_kv_append(void* k_cache, void* v_cache, int kv_dtype, int NB, int BS,
+                     int64_t row_elems, const int32_t* bt, int MB, const int32_t* positions,
+                     const int32_t* seq_ids, int64_t n, const void* k_src, const void* v_src,
+                     int src_dtype, int64_t src_row_stride, hipStream_t stream);
+
 // Matrix-core causal prefill (hs_prefill_mfma.hip).  cu_q null: S rows per
 // sequence, q/out [B, S, H, D]; else ragged rows as in hs_prefill_varlen.
 int launch_prefill_mfma(const float* q, const int32_t* cu_q, int S, int max_rows_per_seq,

@@ -54,6 +54,10 @@ _SIGNATURES = {
     "hs_kv_unpack": (_c_int, [_c_vp, _c_int, _c_int, _c_i64, _c_vp, _c_int, _c_vp, _c_vp]),
     "hs_kv_gather": (_c_int, [_c_vp, _c_int, _c_int, _c_i64, _c_vp, _c_int, _c_int, _c_int,
                               _c_vp, _c_vp]),
+    "hs_kv_scatter": (_c_int, [_c_vp, _c_vp, _c_int, _c_i64, _c_int, _c_int, _c_vp, _c_i64,
+                               _c_vp, _c_vp, _c_int, _c_i64, _c_vp]),
+    "hs_kv_append": (_c_int, [_c_vp, _c_vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_vp,
+                              _c_int, _c_vp, _c_vp, _c_i64, _c_vp, _c_vp, _c_int, _c_i64, _c_vp]),
 }
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)
@@ -345,3 +349,93 @@ def kv_gather(cache, block_tables_dev, length: int, out) -> None:
     with _DeviceGuard(cache.device):
         check(L.hs_kv_gather(cache.data_ptr(), NB, BS, row, block_tables_dev.data_ptr(), MB,
                              B, int(length), out.data_ptr(), stream_of(cache.device)))
+
+
+def _rows(x, Hkv: int, D: int):
+    """(tensor, row stride in elements) of new K or V rows [n, Hkv, D].
+
+    Accepts [n, Hkv, D] or [n, Hkv * D]; the rows may be strided (a slice of
+    the fused QKV output) but each row's Hkv * D elements must be contiguous.
+    """
+    if x.dim() == 3:
+        if tuple(x.shape[1:]) != (Hkv, D):
+            raise RuntimeError(f"K/V rows must be [n, {Hkv}, {D}], got {tuple(x.shape)}")
+        row_ok = x.stride(2) == 1 and x.stride(1) == D
+    elif x.dim() == 2:
+        if x.shape[1] != Hkv * D:
+            raise RuntimeError(f"K/V rows must be [n, {Hkv * D}], got {tuple(x.shape)}")
+        row_ok = x.stride(1) == 1
+    else:
+        raise RuntimeError(f"K/V rows must be [n, Hkv, D], got {tuple(x.shape)}")
+    if not row_ok:
+        x = x.contiguous()
+    stride = x.stride(0) if x.shape[0] > 1 else Hkv * D
+    return x, stride
+
+
+def _check_write(k_cache, v_cache, k, v):
+    """The caches are written in place: CUDA, contiguous, same shape/dtype."""
+    if k_cache.dim() != 4:
+        raise RuntimeError("k_cache must be [NB, BS, Hkv, D]")
+    if v_cache.shape != k_cache.shape or v_cache.dtype != k_cache.dtype:
+        raise RuntimeError("k_cache and v_cache must have the same shape and dtype")
+    if not (k_cache.is_cuda and v_cache.is_cuda and k.is_cuda and v.is_cuda):
+        raise RuntimeError("kv cache and new rows must be on CUDA")
+    if len({k_cache.device, v_cache.device, k.device, v.device}) != 1:
+        raise RuntimeError("kv cache and new rows must be on the same device")
+    if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+        raise RuntimeError("kv cache must be contiguous (it is written in place)")
+
+
+def _same_rows(k, v, Hkv: int, D: int):
+    k, ks = _rows(k, Hkv, D)
+    v, vs = _rows(v, Hkv, D)
+    if k.shape[0] != v.shape[0] or k.dtype != v.dtype:
+        raise RuntimeError("k and v rows must have the same count and dtype")
+    if ks != vs:
+        k, v = k.contiguous(), v.contiguous()
+        ks = vs = Hkv * D
+    return k, v, ks
+
+
+def kv_scatter(k_cache, v_cache, slots, k, v) -> None:
+    """k_cache.view(-1, Hkv, D)[slots] = k.to(cache dtype); same for v."""
+    L = lib("KV scatter HIP kernel")
+    _check_write(k_cache, v_cache, k, v)
+    NB, BS, Hkv, D = k_cache.shape
+    k, v, stride = _same_rows(k, v, Hkv, D)
+    n = k.shape[0]
+    if slots.numel() != n:
+        raise RuntimeError(f"{slots.numel()} slots for {n} rows")
+    import torch
+
+    slots = torch.as_tensor(slots).to(device=k_cache.device, dtype=torch.int64).contiguous()
+    with _DeviceGuard(k_cache.device):
+        check(L.hs_kv_scatter(k_cache.data_ptr(), v_cache.data_ptr(), dtype_code(k_cache.dtype),
+                              NB * BS, Hkv, D, slots.data_ptr(), n, k.data_ptr(), v.data_ptr(),
+                              dtype_code(k.dtype), stride, stream_of(k_cache.device)))
+
+
+def kv_append(k_cache, v_cache, block_tables, positions, k, v, seq_ids=None) -> None:
+    """Row i -> slot block_tables[s][pos // BS] * BS + pos % BS of sequence
+    s = seq_ids[i] (or i), pos = positions[i]; cast as kv_scatter."""
+    L = lib("KV append HIP kernel")
+    _check_write(k_cache, v_cache, k, v)
+    NB, BS, Hkv, D = k_cache.shape
+    k, v, stride = _same_rows(k, v, Hkv, D)
+    n = k.shape[0]
+    dev = k_cache.device
+    bt = _int32_on(block_tables, dev)
+    pos = _int32_on(positions, dev)
+    if pos.numel() != n:
+        raise RuntimeError(f"{pos.numel()} positions for {n} rows")
+    sid = None if seq_ids is None else _int32_on(seq_ids, dev)
+    if sid is not None and sid.numel() != n:
+        raise RuntimeError(f"{sid.numel()} sequence ids for {n} rows")
+    if sid is None and n > bt.shape[0]:
+        raise RuntimeError("without seq_ids, row i uses table row i: more rows than tables")
+    with _DeviceGuard(dev):
+        check(L.hs_kv_append(k_cache.data_ptr(), v_cache.data_ptr(), dtype_code(k_cache.dtype), NB,
+                             BS, Hkv, D, bt.data_ptr(), bt.shape[1], pos.data_ptr(),
+                             None if sid is None else sid.data_ptr(), n, k.data_ptr(),
+                             v.data_ptr(), dtype_code(k.dtype), stride, stream_of(dev)))

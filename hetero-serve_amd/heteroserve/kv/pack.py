@@ -9,6 +9,9 @@ format both of the reference's transports carry.
     export_blocks_device  pool -> payload   torch_blocks.py:137-148
     write_blocks_device   payload -> pool   torch_blocks.py:150-154
     gather_kv_batch       pool layer -> [B, length, Hkv, D]   torch_blocks.py:125-135
+    scatter_kv            new K/V rows -> their slots   torch_engine.py:239-240, :306-308
+    append_kv             new K/V rows -> slots from block tables and positions
+    write_kv              [L, H, T, D] K/V -> pool   torch_blocks.py:89-106
 
 Each is one libhsattn launch (a bitwise page copy) instead of the reference's
 advanced-index gather plus permute-copy, or its Python loop of one copy per
@@ -134,13 +137,78 @@ def gather_kv_batch(pool, tables, length: int, layer: int):
     return k_out, v_out
 
 
+def slots_for(block_ids, positions, block_size: int):
+    """Flat slots of absolute token positions through one block table
+    (torch_blocks.py:68-73): ``table[pos // BS] * BS + pos % BS``, int64."""
+    import torch
+
+    tbl = torch.as_tensor(block_ids, dtype=torch.long)
+    pos = torch.as_tensor(positions, dtype=torch.long)
+    return tbl[pos // block_size] * block_size + (pos % block_size)
+
+
+def scatter_kv(k_cache, v_cache, slots, k, v) -> None:
+    """``fk[slots] = k.to(dtype); fv[slots] = v.to(dtype)`` for one layer's caches
+    ``[NB, BS, Hkv, D]`` and new rows ``[n, Hkv, D]`` (torch_engine.py:239-240,
+    :306-308), in one launch.  Rows may be a strided view such as a slice of
+    the fused QKV output.  Negative slots count from the end, as in torch
+    indexing.  Host slots (a list or CPU tensor) outside [-NB*BS, NB*BS) raise
+    IndexError before the launch; device slots are not read back (that would
+    stall the step), and a device slot out of range is not written.  Slots
+    must not repeat (as in the engine: one token per slot per step).
+    """
+    import torch
+
+    n_slots = k_cache.shape[0] * k_cache.shape[1]
+    on_host = not (torch.is_tensor(slots) and slots.is_cuda)
+    slots = torch.as_tensor(slots, dtype=torch.long)
+    if on_host and slots.numel():
+        lo, hi = int(slots.min()), int(slots.max())
+        if lo < -n_slots or hi >= n_slots:
+            bad = lo if lo < -n_slots else hi
+            raise IndexError(f"index {bad} is out of bounds for dimension 0 with size {n_slots}")
+    slots = torch.where(slots < 0, slots + n_slots, slots)
+    _hip.kv_scatter(k_cache, v_cache, slots, k, v)
+
+
+def append_kv(k_cache, v_cache, block_tables, positions, k, v, seq_ids=None) -> None:
+    """Write row i at absolute position ``positions[i]`` of sequence
+    ``seq_ids[i]`` (row i of the tables when None), slots computed on the GPU
+    from the int32 ``[B, MB]`` block tables.  Replaces the engine's
+    per-sequence slot loop (torch_engine.py:221-227, a device-to-host copy per
+    sequence) and the scatter after it.  Rows whose position is past the
+    table or whose table entry is padding (-1) are not written.
+    """
+    _hip.kv_append(k_cache, v_cache, block_tables, positions, k, v, seq_ids)
+
+
+def write_kv(pool, block_ids, start_pos: int, k, v) -> None:
+    """``TorchBlockAllocator.write_kv`` (torch_blocks.py:89-106): scatter
+    ``[L, Hkv, T, D]`` K/V of one sequence into every layer of the pool at
+    positions ``start_pos .. start_pos + T - 1``; one launch per layer."""
+    import torch
+
+    _check_pool(pool)
+    L, _, NB, BS, H, D = pool.shape
+    k = torch.as_tensor(k, device=pool.device)
+    v = torch.as_tensor(v, device=pool.device)
+    T = int(k.shape[2])
+    if T == 0:
+        return
+    slots = slots_for(block_ids, range(start_pos, start_pos + T), BS).to(pool.device)
+    kt = k.permute(0, 2, 1, 3).contiguous()      # [L, T, H, D]: token-major rows
+    vt = v.permute(0, 2, 1, 3).contiguous()
+    for layer in range(L):
+        scatter_kv(pool[layer, 0], pool[layer, 1], slots, kt[layer], vt[layer])
+
+
 class HipKVMixin:
     """GPU storage methods for hetero-serve's TorchBlockAllocator.
 
     Expects ``self.pool`` (the device pool), ``self.device`` and
     ``self.torch_dtype`` as TorchBlockAllocator defines them
-    (torch_blocks.py:33-48).  Overrides the methods of torch_blocks.py:125-175
-    that move KV pages.
+    (torch_blocks.py:33-48).  Overrides the methods of torch_blocks.py:89-175
+    that write or move KV pages.
     """
 
     def export_blocks_device(self, block_ids):
@@ -163,3 +231,6 @@ class HipKVMixin:
 
     def gather_kv_batch(self, tables, length: int, layer: int):
         return gather_kv_batch(self.pool, tables, length, layer)
+
+    def write_kv(self, block_ids, start_pos, k, v) -> None:
+        write_kv(self.pool, block_ids, start_pos, k, v)

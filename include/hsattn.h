@@ -194,6 +194,41 @@ int hs_kv_gather(const void* cache, int NB, int BS, int64_t row_bytes,
                  const int32_t* block_tables, int MB, int B, int length, void* out,
                  void* stream);
 
+/*
+ * Write new K and V rows into one layer's cache:
+ *   k_cache[slots[i]] = cast(k_src[i]),  v_cache[slots[i]] = cast(v_src[i])
+ * for i < n, where a cache is [num_slots, Hkv, D] (the pool view
+ * [NB, BS, Hkv, D] with num_slots = NB * BS) and row i of a source starts
+ * src_row_stride elements after row i - 1 (a strided view of the fused QKV
+ * projection works as is).  Casts round as torch's `.to()` does; equal dtypes
+ * copy bits.  Slots outside [0, num_slots) are skipped; slots must not repeat.
+ * Replaces: fk[slots] = k.to(dtype); fv[slots] = v.to(dtype),
+ *           heteroserve/model/torch_engine.py:239-240 and :306-308, and the
+ *           per-layer loop of TorchBlockAllocator.write_kv,
+ *           heteroserve/kv/torch_blocks.py:89-106.
+ */
+int hs_kv_scatter(void* k_cache, void* v_cache, int kv_dtype, int64_t num_slots, int Hkv, int D,
+                  const int64_t* slots, int64_t n, const void* k_src, const void* v_src,
+                  int src_dtype, int64_t src_row_stride, void* stream);
+
+/*
+ * hs_kv_scatter with each row's slot computed on the device from its
+ * sequence's block table (int32 [B, MB], -1 padded) and its absolute
+ * position:  slot = block_tables[s][pos / BS] * BS + pos % BS,  with
+ * s = seq_ids[i] (or s = i when seq_ids is NULL) and pos = positions[i].
+ * Rows whose position is negative or past the table, or whose table entry is
+ * outside [0, NB), are skipped.
+ * Replaces: the per-sequence slot loop of decode_batch_paged
+ *           (heteroserve/model/torch_engine.py:221-227, one .tolist() per
+ *           sequence) followed by the scatter at :239-240; and
+ *           TorchBlockAllocator.slots_for + write_kv
+ *           (heteroserve/kv/torch_blocks.py:68-73, 89-106) for a chunk.
+ */
+int hs_kv_append(void* k_cache, void* v_cache, int kv_dtype, int NB, int BS, int Hkv, int D,
+                 const int32_t* block_tables, int MB, const int32_t* positions,
+                 const int32_t* seq_ids, int64_t n, const void* k_src, const void* v_src,
+                 int src_dtype, int64_t src_row_stride, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

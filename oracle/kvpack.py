@@ -46,3 +46,53 @@ def gather_kv_batch(pool: np.ndarray, tables, length: int, layer: int):
     shape = (0, length, h, d)
     return (np.stack(ks) if ks else np.zeros(shape, pool.dtype),
             np.stack(vs) if vs else np.zeros(shape, pool.dtype))
+
+
+# ---------------------------------------------------------------------------
+# writing new K/V rows (the step before attention)
+# ---------------------------------------------------------------------------
+
+def slots_for(block_ids, positions, block_size: int) -> np.ndarray:
+    """Flat slots of absolute positions through one block table, int64.
+
+    heteroserve/kv/torch_blocks.py:68-73: tbl[pos // BS] * BS + pos % BS.
+    """
+    tbl = np.asarray(list(block_ids), dtype=np.int64)
+    pos = np.asarray(list(positions), dtype=np.int64)
+    return tbl[pos // block_size] * block_size + pos % block_size
+
+
+def scatter_rows(cache, slots, rows) -> None:
+    """cache.view(-1, H, D)[slots] = rows.to(cache dtype), on CPU torch.
+
+    The engine's write of one step's new K (or V), heteroserve/model/
+    torch_engine.py:239-240 (decode) and :306-308 (a prefill chunk): `cache`
+    is one layer's [NB, BS, H, D] pool view, `rows` is [n, H, D].  torch's
+    `.to()` supplies the rounding (round to nearest even).
+    """
+    import torch
+
+    flat = cache.reshape(-1, cache.shape[2], cache.shape[3])
+    flat[torch.as_tensor(slots, dtype=torch.long)] = torch.as_tensor(rows).to(cache.dtype)
+
+
+def write_kv(pool, block_ids, start_pos: int, k, v) -> None:
+    """TorchBlockAllocator.write_kv, heteroserve/kv/torch_blocks.py:89-106.
+
+    pool [L, 2, NB, BS, H, D] (CPU torch); k, v [L, H, T, D] of one sequence
+    written at positions start_pos .. start_pos + T - 1 of every layer.
+    """
+    import torch
+
+    k = torch.as_tensor(k)
+    v = torch.as_tensor(v)
+    T = int(k.shape[2])
+    if T == 0:
+        return
+    bs = pool.shape[3]
+    slots = slots_for(block_ids, range(start_pos, start_pos + T), bs)
+    kt = k.permute(0, 2, 1, 3).contiguous()
+    vt = v.permute(0, 2, 1, 3).contiguous()
+    for layer in range(pool.shape[0]):
+        scatter_rows(pool[layer, 0], slots, kt[layer])
+        scatter_rows(pool[layer, 1], slots, vt[layer])

@@ -82,6 +82,20 @@ def test_argument_errors_need_no_device(lib):
     rc = lib.hs_profile_next_launch(fake, None)
     assert rc == -1
     assert lib.hs_profile_next_launch(None, None) == 0
+    # writes of new K/V rows
+    rc = lib.hs_kv_scatter(fake, fake, 2, 128, 4, 64, fake, 3, fake, fake, 0, 100, None)
+    assert rc == -1 and b"stride" in lib.hs_last_error()
+    rc = lib.hs_kv_scatter(fake, fake, 7, 128, 4, 64, fake, 3, fake, fake, 0, 256, None)
+    assert rc == -1 and b"dtype" in lib.hs_last_error()
+    rc = lib.hs_kv_scatter(fake, fake, 2, 128, 4, 64, None, 3, fake, fake, 0, 256, None)
+    assert rc == -1 and b"null" in lib.hs_last_error()
+    assert lib.hs_kv_scatter(None, None, 2, 128, 4, 64, None, 0, None, None, 0, 256, None) == 0
+    rc = lib.hs_kv_append(fake, fake, 2, 8, 0, 4, 64, fake, 2, fake, None, 3, fake, fake, 0,
+                          256, None)
+    assert rc == -1 and b"positive" in lib.hs_last_error()
+    rc = lib.hs_kv_append(fake, fake, 2, 8, 16, 4, 64, None, 2, fake, None, 3, fake, fake, 0,
+                          256, None)
+    assert rc == -1 and b"null" in lib.hs_last_error()
 
 
 def test_workspace_size_formula(lib):

@@ -101,6 +101,68 @@ def check_pack_by_loops(export_fn):
                             assert got[i, l, c, t, h, d] == pool[l, c, blk % 7, t, h, d]
 
 
+def bf16_bits(x: np.ndarray) -> np.ndarray:
+    """fp32 -> bf16 bit patterns, round to nearest even (non-NaN inputs)."""
+    b = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    return ((b + 0x7FFF + ((b >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def check_slots_by_loop(slots_fn):
+    rng = np.random.default_rng(3)
+    for bs in (1, 4, 16):
+        table = rng.permutation(40)[:9].tolist()
+        pos = rng.integers(0, 9 * bs, size=25)
+        got = slots_fn(table, pos, bs)
+        for i, p_ in enumerate(pos):
+            assert got[i] == table[p_ // bs] * bs + p_ % bs
+
+
+def check_scatter_by_loops(scatter_fn):
+    """Each written row equals its source row rounded independently (numpy's
+    fp16 cast, the bf16 bit formula); rows not written stay zero."""
+    rng = np.random.default_rng(4)
+    nb, bs, h, d = 5, 4, 3, 8
+    src = (rng.standard_normal((7, h, d)) * 3).astype(np.float32)
+    src[0, 0, :6] = [np.inf, -np.inf, 65520.0, 65519.0, 1e-8, -3e-5]   # fp16 edges
+    src[1, 0, 0] = np.float32(1.0) + np.float32(2 ** -8)               # a bf16 tie
+    slots = rng.permutation(nb * bs)[:7]
+    for dt in (torch.float32, torch.float16, torch.bfloat16):
+        cache = torch.zeros(nb, bs, h, d, dtype=dt)
+        scatter_fn(cache, slots, torch.as_tensor(src))
+        flat = cache.reshape(-1, h, d)
+        written = set(int(x) for x in slots)
+        for i, sl in enumerate(slots):
+            row = flat[int(sl)]
+            if dt == torch.float32:
+                assert np.array_equal(row.numpy(), src[i])
+            elif dt == torch.float16:
+                with np.errstate(over="ignore"):          # 65520 rounds to inf, as intended
+                    want = src[i].astype(np.float16)
+                assert np.array_equal(row.numpy(), want)
+            else:
+                assert np.array_equal(row.view(torch.int16).numpy().view(np.uint16),
+                                      bf16_bits(src[i]))
+        for sl in range(nb * bs):
+            if sl not in written:
+                assert not flat[sl].any()
+
+
+def check_write_kv_round_trip(write_fn):
+    """write_kv, then a gather through the same table, returns the rows."""
+    rng = np.random.default_rng(5)
+    L, nb, bs, h, d = 2, 9, 4, 3, 8
+    pool = torch.zeros(L, 2, nb, bs, h, d)
+    table = [6, 1, 8, 3]
+    k = torch.as_tensor(rng.standard_normal((L, h, 11, d)).astype(np.float32))
+    v = torch.as_tensor(rng.standard_normal((L, h, 11, d)).astype(np.float32))
+    write_fn(pool, table, 3, k, v)
+    for layer in range(L):
+        gk, gv = kvp.gather_kv_batch(pool.numpy(), [table], 14, layer)
+        assert np.array_equal(gk[0, 3:], k[layer].permute(1, 0, 2).numpy())
+        assert np.array_equal(gv[0, 3:], v[layer].permute(1, 0, 2).numpy())
+        assert not gk[0, :3].any() and not gv[0, :3].any()
+
+
 # ---------------------------------------------------------------------------
 # the oracle against the mathematics
 # ---------------------------------------------------------------------------
@@ -283,6 +345,18 @@ def test_pack_oracle():
     assert np.array_equal(dst[:, :, 3], payload[1])
 
 
+def test_kv_write_oracle():
+    """slots_for, the engine's scatter and write_kv (torch_blocks.py:68-106,
+    torch_engine.py:239-240)."""
+    check_slots_by_loop(kvp.slots_for)
+    check_scatter_by_loops(kvp.scatter_rows)
+    check_write_kv_round_trip(kvp.write_kv)
+    # NaN stays NaN (torch's encodings of it differ between its code paths)
+    cache = torch.zeros(1, 2, 1, 2, dtype=torch.bfloat16)
+    kvp.scatter_rows(cache, [1], torch.tensor([[[float("nan"), 1.0]]]))
+    assert torch.isnan(cache[0, 1, 0, 0]) and cache[0, 1, 0, 1] == 1.0
+
+
 def test_split_heuristic_known_answers():
     """The reference's recorded runs on a 40-SM T4 (README:336, :346) and the
     formula's clamps."""
@@ -328,6 +402,12 @@ MUTANTS = [
      "key_end = min(ctx_len, pos0 + 1)", "tiled"),
     ("pack axes", kvp, "np.moveaxis(pool[:, :, idx], 2, 0)", "np.moveaxis(pool[:, :, idx], 2, 1)",
      "pack"),
+    ("slot offset within a block", kvp, "tbl[pos // block_size] * block_size + pos % block_size",
+     "tbl[pos // block_size] * block_size + (pos + 1) % block_size", "slots"),
+    ("rows not made token-major", kvp, "kt = k.permute(0, 2, 1, 3).contiguous()",
+     "kt = k.reshape(k.shape[0], k.shape[2], k.shape[1], k.shape[3])", "write_kv"),
+    ("write position from zero", kvp, "range(start_pos, start_pos + T)", "range(0, T)",
+     "write_kv"),
 ]
 
 
@@ -347,6 +427,10 @@ def _run_check(kind, mod):
             check_tiled_vs_dense(mod.tiled_prefill_reference, ctx, S, D)
     elif kind == "pack":
         check_pack_by_loops(mod.export_blocks)
+    elif kind == "slots":
+        check_slots_by_loop(mod.slots_for)
+    elif kind == "write_kv":
+        check_write_kv_round_trip(mod.write_kv)
 
 
 @pytest.mark.parametrize("name,module,old,new,kind", MUTANTS, ids=[m[0] for m in MUTANTS])
