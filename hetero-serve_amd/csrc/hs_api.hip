@@ -348,4 +348,11 @@ int hs_kv_append(void* k_cache, void* v_cache, int kv_dtype, int NB, int BS, int
                           static_cast<hipStream_t>(stream));
 }
 
+int hs_block_tables(const int32_t* packed, int B, int width, int32_t* out, void* stream) {
+  if (B < 0 || width < 0) return fail(HS_EINVAL, "block table sizes must be non-negative");
+  if ((int64_t)B * width == 0) return HS_OK;
+  if (!packed || !out) return fail(HS_EINVAL, "null pointer");
+  return launch_block_tables(packed, B, width, out, static_cast<hipStream_t>(stream));
+}
+
 }  // extern "C"

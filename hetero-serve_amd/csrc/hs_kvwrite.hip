@@ -270,6 +270,30 @@ int launch_kv_write(void* k_cache, void* v_cache, int kv_dtype, const void* k_sr
 
 }  // namespace
 
+// out[b, j] = ids[off[b] + j] for j < off[b+1] - off[b] (capped at width), else
+// -1; packed = [off[0..B], ids...] uploaded in one copy.
+__global__ __launch_bounds__(kWriteThreads) void block_tables_kernel(const int32_t* packed, int B,
+                                                                    int width, int32_t* out) {
+  const int64_t g = (int64_t)blockIdx.x * kWriteThreads + threadIdx.x;
+  if (g >= (int64_t)B * width) return;
+  const int b = (int)(g / width);
+  const int j = (int)(g - (int64_t)b * width);
+  const int off = packed[b];
+  const int len = packed[b + 1] - off;
+  out[g] = j < len ? packed[B + 1 + off + j] : -1;
+}
+
+int launch_block_tables(const int32_t* packed, int B, int width, int32_t* out,
+                        hipStream_t stream) {
+  const int64_t work = (int64_t)B * width;
+  if (work == 0) return HS_OK;
+  if ((work + kWriteThreads - 1) / kWriteThreads > 0x7fffffffLL)
+    return fail(HS_EUNSUPPORTED, "block table too large for one launch");
+  hipLaunchKernelGGL(block_tables_kernel, dim3((unsigned)((work + kWriteThreads - 1) / kWriteThreads)),
+                     dim3(kWriteThreads), 0, stream, packed, B, width, out);
+  return check_launch("block table build");
+}
+
 int launch_kv_scatter(void* k_cache, void* v_cache, int kv_dtype, int64_t num_slots,
                       int64_t row_elems, const int64_t* slots, int64_t n, const void* k_src,
                       const void* v_src, int src_dtype, int64_t src_row_stride,

@@ -54,6 +54,7 @@ _SIGNATURES = {
     "hs_kv_unpack": (_c_int, [_c_vp, _c_int, _c_int, _c_i64, _c_vp, _c_int, _c_vp, _c_vp]),
     "hs_kv_gather": (_c_int, [_c_vp, _c_int, _c_int, _c_i64, _c_vp, _c_int, _c_int, _c_int,
                               _c_vp, _c_vp]),
+    "hs_block_tables": (_c_int, [_c_vp, _c_int, _c_int, _c_vp, _c_vp]),
     "hs_kv_scatter": (_c_int, [_c_vp, _c_vp, _c_int, _c_i64, _c_int, _c_int, _c_vp, _c_i64,
                                _c_vp, _c_vp, _c_int, _c_i64, _c_vp]),
     "hs_kv_append": (_c_int, [_c_vp, _c_vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_vp,
@@ -439,3 +440,11 @@ def kv_append(k_cache, v_cache, block_tables, positions, k, v, seq_ids=None) -> 
                              BS, Hkv, D, bt.data_ptr(), bt.shape[1], pos.data_ptr(),
                              None if sid is None else sid.data_ptr(), n, k.data_ptr(),
                              v.data_ptr(), dtype_code(k.dtype), stride, stream_of(dev)))
+
+
+def block_tables(packed_dev, B: int, width: int, out) -> None:
+    """out[B, width] int32 from the packed [off[0..B], ids...] device buffer."""
+    L = lib("block table HIP kernel")
+    with _DeviceGuard(out.device):
+        check(L.hs_block_tables(packed_dev.data_ptr(), B, width, out.data_ptr(),
+                                stream_of(out.device)))

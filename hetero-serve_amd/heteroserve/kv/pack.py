@@ -12,6 +12,7 @@ format both of the reference's transports carry.
     scatter_kv            new K/V rows -> their slots   torch_engine.py:239-240, :306-308
     append_kv             new K/V rows -> slots from block tables and positions
     write_kv              [L, H, T, D] K/V -> pool   torch_blocks.py:89-106
+    block_table_tensor    tables -> [B, width] int32   torch_blocks.py:75-85
 
 Each is one libhsattn launch (a bitwise page copy) instead of the reference's
 advanced-index gather plus permute-copy, or its Python loop of one copy per
@@ -202,6 +203,31 @@ def write_kv(pool, block_ids, start_pos: int, k, v) -> None:
         scatter_kv(pool[layer, 0], pool[layer, 1], slots, kt[layer], vt[layer])
 
 
+def block_table_tensor(tables, pad_to=None, device="cuda"):
+    """``TorchBlockAllocator.block_table_tensor`` (torch_blocks.py:75-85): an
+    int32 ``[len(tables), width]`` table, -1 padded, ``width = pad_to`` or the
+    longest table (1 when there are no tables); longer tables are truncated.
+    One host-to-device copy of all ids instead of one per sequence."""
+    import numpy as np
+    import torch
+
+    tables = [list(t) for t in tables]
+    width = pad_to or max((len(t) for t in tables), default=1)
+    B = len(tables)
+    out = torch.empty((B, width), dtype=torch.int32, device=device)
+    if B == 0 or width == 0:
+        return out
+    rows = [np.asarray(t[:width], dtype=np.int64) for t in tables]
+    flat = np.concatenate(rows) if rows else np.zeros(0, np.int64)
+    if flat.size and (flat.min() < -2 ** 31 or flat.max() >= 2 ** 31):
+        raise RuntimeError("value cannot be converted to type int32 without overflow")
+    off = np.zeros(B + 1, dtype=np.int64)
+    np.cumsum([r.size for r in rows], out=off[1:])
+    packed = torch.from_numpy(np.concatenate([off, flat]).astype(np.int32)).to(out.device)
+    _hip.block_tables(packed, B, width, out)
+    return out
+
+
 class HipKVMixin:
     """GPU storage methods for hetero-serve's TorchBlockAllocator.
 
@@ -234,3 +260,6 @@ class HipKVMixin:
 
     def write_kv(self, block_ids, start_pos, k, v) -> None:
         write_kv(self.pool, block_ids, start_pos, k, v)
+
+    def block_table_tensor(self, tables, pad_to=None):
+        return block_table_tensor(tables, pad_to, self.device)

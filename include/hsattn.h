@@ -229,6 +229,18 @@ int hs_kv_append(void* k_cache, void* v_cache, int kv_dtype, int NB, int BS, int
                  const int32_t* seq_ids, int64_t n, const void* k_src, const void* v_src,
                  int src_dtype, int64_t src_row_stride, void* stream);
 
+/*
+ * Build the int32 block-table tensor [B, width], -1 padded, from one device
+ * buffer packed = [off[0], ..., off[B], ids...]: row b holds
+ * ids[off[b] .. off[b+1]) truncated to `width` entries.  The host uploads
+ * the buffer in one copy.
+ * Replaces: TorchBlockAllocator.block_table_tensor,
+ *           heteroserve/kv/torch_blocks.py:75-85 (one host-to-device copy per
+ *           sequence), called every decode step at
+ *           heteroserve/model/torch_engine.py:215-216.
+ */
+int hs_block_tables(const int32_t* packed, int B, int width, int32_t* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -96,3 +96,16 @@ def write_kv(pool, block_ids, start_pos: int, k, v) -> None:
     for layer in range(pool.shape[0]):
         scatter_rows(pool[layer, 0], slots, kt[layer])
         scatter_rows(pool[layer, 1], slots, vt[layer])
+
+
+def block_table_tensor(tables, pad_to=None):
+    """TorchBlockAllocator.block_table_tensor, heteroserve/kv/torch_blocks.py:75-85,
+    on CPU torch: [len(tables), width] int32, -1 padded, rows truncated to width."""
+    import torch
+
+    width = pad_to or max((len(t) for t in tables), default=1)
+    out = torch.full((len(tables), width), -1, dtype=torch.int32)
+    for i, t in enumerate(tables):
+        if t:
+            out[i, : len(t)] = torch.as_tensor(list(t)[:width], dtype=torch.int32)
+    return out

@@ -1,4 +1,5 @@
-"""GPU parity of writing new K/V rows into the paged cache.
+"""GPU parity of writing new K/V rows into the paged cache, and of building
+the block-table tensor the kernels walk.
 
 hs_kv_scatter / hs_kv_append against the oracle's restatement of the
 engine's ``fk[slots] = k.to(dtype)`` (torch_engine.py:239-240, :306-308) and
@@ -182,3 +183,19 @@ def test_host_slots_are_checked_and_empty_writes_are_noops():
     pk.scatter_kv(gk, gv, torch.empty(0, dtype=torch.long), rows[:0], rows[:0])
     with pytest.raises(RuntimeError):
         pk.scatter_kv(gk, gv, [1, 2], torch.ones(2, 3, 32, device=DEV), rows)
+
+
+def test_block_table_tensor_matches_reference():
+    """block_table_tensor (torch_blocks.py:75-85) built on the GPU from one
+    upload: C5's 255 sequences, explicit widths (padding and truncation) and
+    empty tables, equal to the reference's loop of per-sequence copies."""
+    pk = _pack()
+    rng = np.random.default_rng(50)
+    tables = [rng.permutation(65536)[: int(n)].tolist() for n in rng.integers(16, 257, size=255)]
+    tables[3] = []
+    for pad_to in (None, 300, 100):
+        got = pk.block_table_tensor(tables, pad_to, DEV)
+        want = kvp.block_table_tensor(tables, pad_to)
+        assert torch.equal(got.cpu(), want)
+    for tbl in ([], [[], []], [[5]], [[1, 2], [3]]):
+        assert torch.equal(pk.block_table_tensor(tbl, None, DEV).cpu(), kvp.block_table_tensor(tbl))

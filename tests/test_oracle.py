@@ -357,6 +357,21 @@ def test_kv_write_oracle():
     assert torch.isnan(cache[0, 1, 0, 0]) and cache[0, 1, 0, 1] == 1.0
 
 
+def test_block_table_oracle():
+    """block_table_tensor (torch_blocks.py:75-85) cell by cell: ids in order,
+    -1 padding, width = pad_to or the longest table, truncation."""
+    tables = [[4, 9, 1], [], [7], [3, 3, 8, 2, 6]]
+    for pad_to in (None, 2, 8):
+        got = kvp.block_table_tensor(tables, pad_to)
+        width = pad_to or 5
+        assert got.dtype == torch.int32 and tuple(got.shape) == (4, width)
+        for i, t in enumerate(tables):
+            for j in range(width):
+                assert int(got[i, j]) == (t[j] if j < len(t) else -1)
+    assert tuple(kvp.block_table_tensor([]).shape) == (0, 1)
+    assert tuple(kvp.block_table_tensor([[], []]).shape) == (2, 0)
+
+
 def test_split_heuristic_known_answers():
     """The reference's recorded runs on a 40-SM T4 (README:336, :346) and the
     formula's clamps."""
