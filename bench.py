@@ -83,7 +83,7 @@ def decode_leg(case, steps: int, warmup: int, partition_tokens: int = 0) -> dict
     NB, BS, Hkv, _ = kc.shape
     MB = case.block_tables.shape[1]
     out = torch.empty((B, H, D), dtype=torch.float32, device=case.q.device)
-    ws_bytes = lib.hs_decode_workspace_bytes(B, H, D, BS, MB, 0, partition_tokens)
+    ws_bytes = lib.hs_decode_workspace_bytes(B, H, Hkv, D, BS, MB, 0, partition_tokens)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=case.q.device)
     stream = torch.cuda.current_stream().cuda_stream
     dt = _hip.dtype_code(kc.dtype)

@@ -15,8 +15,9 @@
 // product is reduced inside one 16-lane DPP row, with no LDS traffic.  Each
 // group of kLpt lanes ("slot") runs its own online softmax over the tokens it
 // loads; the kTpl slot states are merged once at the end of the partition.
-// A workgroup is kWaves waves = consecutive heads of the same (row,
-// partition), and the head group is the fastest-varying grid index, so the
+// A workgroup is kDecodeWaves waves = consecutive heads (or GQA head groups)
+// of the same (row, partition), and the head group is the fastest-varying grid
+// index, so the
 // workgroups in flight together stream whole token rows (all heads of a token
 // are adjacent in the page) instead of one head's narrow column of many rows.
 // KV loads are non-temporal: every byte is read once, so it should not
@@ -71,22 +72,30 @@ __device__ inline bool partition_range(const RowAttnArgs& a, int end, int p, int
   return p < nparts;
 }
 
-constexpr int kDecodeWaves = 2;  // heads per workgroup
+constexpr int kDecodeWaves = 2;  // waves per workgroup
 
-template <typename T, int D, bool kPaged>
+// One wave = G query heads of one KV group for one (row, partition): each
+// 16-byte K/V load feeds G dot products, so a GQA group's pages are read once
+// instead of once per query head.  G = 1 is plain multi-head attention.  The
+// arithmetic of each head is the same for every G (same slots, token order
+// and reduction order), so packing does not change results.
+template <typename T, int D, bool kPaged, int G>
 __global__ __launch_bounds__(kDecodeWaves * 64) void row_attn_part_kernel(RowAttnArgs a) {
   constexpr int kVec = Elem<T>::kVec;
   constexpr int kLpt = D / kVec;           // lanes per token
   constexpr int kTpl = 64 / kLpt;          // tokens per wave-wide load
-  constexpr int kU = kTpl >= 32 ? 1 : (32 / kTpl < 8 ? 32 / kTpl : 8);  // loads in flight
+  constexpr int kU0 = kTpl >= 32 ? 1 : (32 / kTpl < 8 ? 32 / kTpl : 8);
+  constexpr int kU = kU0 / G > 1 ? kU0 / G : 1;   // loads in flight (registers shrink with G)
   constexpr int kStep = kTpl * kU;         // tokens per loop iteration
   static_assert(kLpt >= 1 && kLpt <= 64 && 64 % kLpt == 0, "head_dim / lane split");
 
   const int lane = threadIdx.x & 63;
-  const int n_groups = (a.H + kDecodeWaves - 1) / kDecodeWaves;
+  const int n_hw = a.H / G;                                     // head groups of G
+  const int n_groups = (n_hw + kDecodeWaves - 1) / kDecodeWaves;
   const int64_t wg = blockIdx.x;
-  const int h = (int)(wg % n_groups) * kDecodeWaves + (threadIdx.x >> 6);
-  if (h >= a.H) return;
+  const int hw = (int)(wg % n_groups) * kDecodeWaves + (threadIdx.x >> 6);
+  if (hw >= n_hw) return;
+  const int h0 = hw * G;                   // first query head of this wave
   const int64_t rp = wg / n_groups;        // row * P + partition
   const int row = (int)(rp / a.P);
   const int p = (int)(rp - (int64_t)row * a.P);
@@ -95,40 +104,46 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void row_attn_part_kernel(RowAtt
   if (!row_geometry(a, row, b, end)) return;
   int lo = 0, hi = 0, nparts = 0;
   const bool live = partition_range(a, end, p, lo, hi, nparts);
-  const int64_t orow = ((int64_t)row * a.H + h) * D;
+  const int64_t orow0 = ((int64_t)row * a.H + h0) * D;
   if (!live) {
-    if (end <= 0 && p == 0) {  // nothing to attend to: a zero row
-      for (int d = lane; d < D; d += 64) a.out[orow + d] = 0.0f;
+    if (end <= 0 && p == 0) {  // nothing to attend to: zero rows
+      for (int d = lane; d < G * D; d += 64) a.out[orow0 + d] = 0.0f;
     }
     return;
   }
 
   const int r = lane / kLpt;  // token slot
   const int c = lane % kLpt;  // element chunk
-  const int kvh = h / (a.H / a.Hkv);
+  const int kvh = h0 / (a.H / a.Hkv);
   const int64_t tok_stride = (int64_t)a.Hkv * D;
   const int64_t blk_stride = tok_stride * a.BS;
   const T* kp = reinterpret_cast<const T*>(a.k) + kvh * D + c * kVec;
   const T* vp = reinterpret_cast<const T*>(a.v) + kvh * D + c * kVec;
   const int32_t* bt = a.bt + (int64_t)b * a.MB;
 
-  float qv[kVec];
-  {
-    const float4* q4 = reinterpret_cast<const float4*>(a.q + orow + c * kVec);
+  float qv[G][kVec];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const float4* q4 = reinterpret_cast<const float4*>(a.q + orow0 + g * D + c * kVec);
 #pragma unroll
     for (int i = 0; i < kVec / 4; ++i) {
       const float4 x = q4[i];
-      qv[4 * i + 0] = x.x * a.qscale;
-      qv[4 * i + 1] = x.y * a.qscale;
-      qv[4 * i + 2] = x.z * a.qscale;
-      qv[4 * i + 3] = x.w * a.qscale;
+      qv[g][4 * i + 0] = x.x * a.qscale;
+      qv[g][4 * i + 1] = x.y * a.qscale;
+      qv[g][4 * i + 2] = x.z * a.qscale;
+      qv[g][4 * i + 3] = x.w * a.qscale;
     }
   }
 
-  float m = kNegBig, l = 0.0f;
-  float acc[kVec];
+  float m[G], l[G];
+  float acc[G][kVec];
 #pragma unroll
-  for (int e = 0; e < kVec; ++e) acc[e] = 0.0f;
+  for (int g = 0; g < G; ++g) {
+    m[g] = kNegBig;
+    l[g] = 0.0f;
+#pragma unroll
+    for (int e = 0; e < kVec; ++e) acc[g][e] = 0.0f;
+  }
 
   // Groups of kTpl tokens start at multiples of kTpl, so with kPaged
   // (BS % kTpl == 0) a group never straddles a page and its block id is
@@ -154,73 +169,88 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void row_attn_part_kernel(RowAtt
       vr[u] = load16_stream(vp + off);
     }
 
-    float sc[kU];
     bool ok[kU];
-    float mx = kNegBig;
 #pragma unroll
     for (int u = 0; u < kU; ++u) {
-      float kf[kVec];
-      Elem<T>::to_f32(kr[u], kf);
-      float d = 0.0f;
-#pragma unroll
-      for (int e = 0; e < kVec; ++e) d = fmaf(qv[e], kf[e], d);
-      d = group_sum<kLpt>(d);
       const int t = t0 + u * kTpl + r;
       ok[u] = (t >= lo) && (t < hi);
-      sc[u] = ok[u] ? d : kNegBig;
-      mx = fmaxf(mx, sc[u]);
     }
-    const float m_new = fmaxf(m, mx);
-    const float corr = fast_exp2(m - m_new);
-    float pu[kU];
-    float psum = 0.0f;
+    float pu[G][kU];
 #pragma unroll
-    for (int u = 0; u < kU; ++u) {
-      pu[u] = ok[u] ? fast_exp2(sc[u] - m_new) : 0.0f;
-      psum += pu[u];
+    for (int g = 0; g < G; ++g) {
+      float sc[kU];
+      float mx = kNegBig;
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        float kf[kVec];
+        Elem<T>::to_f32(kr[u], kf);
+        float d = 0.0f;
+#pragma unroll
+        for (int e = 0; e < kVec; ++e) d = fmaf(qv[g][e], kf[e], d);
+        d = group_sum<kLpt>(d);
+        sc[u] = ok[u] ? d : kNegBig;
+        mx = fmaxf(mx, sc[u]);
+      }
+      const float m_new = fmaxf(m[g], mx);
+      const float corr = fast_exp2(m[g] - m_new);
+      float psum = 0.0f;
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        pu[g][u] = ok[u] ? fast_exp2(sc[u] - m_new) : 0.0f;
+        psum += pu[g][u];
+      }
+      l[g] = fmaf(l[g], corr, psum);
+#pragma unroll
+      for (int e = 0; e < kVec; ++e) acc[g][e] *= corr;
+      m[g] = m_new;
     }
-    l = fmaf(l, corr, psum);
-#pragma unroll
-    for (int e = 0; e < kVec; ++e) acc[e] *= corr;
 #pragma unroll
     for (int u = 0; u < kU; ++u) {
       float vf[kVec];
       Elem<T>::to_f32(vr[u], vf);
 #pragma unroll
-      for (int e = 0; e < kVec; ++e) acc[e] = fmaf(pu[u], vf[e], acc[e]);
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int e = 0; e < kVec; ++e) acc[g][e] = fmaf(pu[g][u], vf[e], acc[g][e]);
     }
-    m = m_new;
   }
 
   // Merge the kTpl slot states: lanes with the same chunk c, different slot.
 #pragma unroll
-  for (int off = kLpt; off < 64; off <<= 1) {
-    const float m_o = __shfl_xor(m, off);
-    const float l_o = __shfl_xor(l, off);
-    const float mm = fmaxf(m, m_o);
-    const float w_s = fast_exp2(m - mm);
-    const float w_o = fast_exp2(m_o - mm);
-    l = l * w_s + l_o * w_o;
+  for (int g = 0; g < G; ++g) {
 #pragma unroll
-    for (int e = 0; e < kVec; ++e) acc[e] = acc[e] * w_s + __shfl_xor(acc[e], off) * w_o;
-    m = mm;
+    for (int off = kLpt; off < 64; off <<= 1) {
+      const float m_o = __shfl_xor(m[g], off);
+      const float l_o = __shfl_xor(l[g], off);
+      const float mm = fmaxf(m[g], m_o);
+      const float w_s = fast_exp2(m[g] - mm);
+      const float w_o = fast_exp2(m_o - mm);
+      l[g] = l[g] * w_s + l_o * w_o;
+#pragma unroll
+      for (int e = 0; e < kVec; ++e) acc[g][e] = acc[g][e] * w_s + __shfl_xor(acc[g][e], off) * w_o;
+      m[g] = mm;
+    }
   }
 
   if (r != 0) return;
-  if (nparts == 1) {
-    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-    float4* o4 = reinterpret_cast<float4*>(a.out + orow + c * kVec);
 #pragma unroll
-    for (int i = 0; i < kVec / 4; ++i)
-      o4[i] = make_float4(acc[4 * i] * inv, acc[4 * i + 1] * inv, acc[4 * i + 2] * inv,
-                          acc[4 * i + 3] * inv);
-  } else {
-    const int64_t pi = ((int64_t)row * a.H + h) * a.P + p;
-    float4* o4 = reinterpret_cast<float4*>(a.part_acc + pi * D + c * kVec);
+  for (int g = 0; g < G; ++g) {
+    const int h = h0 + g;
+    if (nparts == 1) {
+      const float inv = l[g] > 0.0f ? 1.0f / l[g] : 0.0f;
+      float4* o4 = reinterpret_cast<float4*>(a.out + orow0 + g * D + c * kVec);
 #pragma unroll
-    for (int i = 0; i < kVec / 4; ++i)
-      o4[i] = make_float4(acc[4 * i], acc[4 * i + 1], acc[4 * i + 2], acc[4 * i + 3]);
-    if (c == 0) *reinterpret_cast<float2*>(a.part_ml + 2 * pi) = make_float2(m, l);
+      for (int i = 0; i < kVec / 4; ++i)
+        o4[i] = make_float4(acc[g][4 * i] * inv, acc[g][4 * i + 1] * inv,
+                            acc[g][4 * i + 2] * inv, acc[g][4 * i + 3] * inv);
+    } else {
+      const int64_t pi = ((int64_t)row * a.H + h) * a.P + p;
+      float4* o4 = reinterpret_cast<float4*>(a.part_acc + pi * D + c * kVec);
+#pragma unroll
+      for (int i = 0; i < kVec / 4; ++i)
+        o4[i] = make_float4(acc[g][4 * i], acc[g][4 * i + 1], acc[g][4 * i + 2], acc[g][4 * i + 3]);
+      if (c == 0) *reinterpret_cast<float2*>(a.part_ml + 2 * pi) = make_float2(m[g], l[g]);
+    }
   }
 }
 
@@ -275,16 +305,34 @@ static int elem_vec(int kv_dtype) { return kv_dtype == HS_DTYPE_F32 ? 4 : 8; }
 // Tokens one wave-wide load covers for this dtype and head_dim.
 int row_attn_tokens_per_load(int kv_dtype, int D) { return 64 / (D / elem_vec(kv_dtype)); }
 
-template <typename T, int D>
-static void launch_typed(const RowAttnArgs& a, dim3 grid, hipStream_t stream) {
+// Query heads per wave: the largest of 1, 2, 4, 8 dividing the GQA group.
+int row_attn_heads_per_wave(int H, int Hkv) {
+  const int group = H / Hkv;
+  int g = 1;
+  while (g < 8 && group % (2 * g) == 0) g *= 2;
+  return g;
+}
+
+template <typename T, int D, int G>
+static void launch_part(const RowAttnArgs& a, hipStream_t stream) {
   const int tpl = 64 / (D / Elem<T>::kVec);
-  profile_begin(stream);
+  const int64_t gx = (int64_t)a.rows * a.P * ((a.H / G + kDecodeWaves - 1) / kDecodeWaves);
+  const dim3 grid((unsigned)gx), block(kDecodeWaves * 64);
   if (a.BS % tpl == 0)
-    hipLaunchKernelGGL((row_attn_part_kernel<T, D, true>), grid, dim3(kDecodeWaves * 64), 0,
-                       stream, a);
+    hipLaunchKernelGGL((row_attn_part_kernel<T, D, true, G>), grid, block, 0, stream, a);
   else
-    hipLaunchKernelGGL((row_attn_part_kernel<T, D, false>), grid, dim3(kDecodeWaves * 64), 0,
-                       stream, a);
+    hipLaunchKernelGGL((row_attn_part_kernel<T, D, false, G>), grid, block, 0, stream, a);
+}
+
+template <typename T, int D>
+static void launch_typed(const RowAttnArgs& a, hipStream_t stream) {
+  profile_begin(stream);
+  switch (row_attn_heads_per_wave(a.H, a.Hkv)) {
+    case 8: launch_part<T, D, 8>(a, stream); break;
+    case 4: launch_part<T, D, 4>(a, stream); break;
+    case 2: launch_part<T, D, 2>(a, stream); break;
+    default: launch_part<T, D, 1>(a, stream); break;
+  }
   profile_end(stream);
   if (a.P > 1) {
     const int64_t waves = (int64_t)a.rows * a.H;
@@ -294,12 +342,12 @@ static void launch_typed(const RowAttnArgs& a, dim3 grid, hipStream_t stream) {
 }
 
 template <typename T>
-static int launch_dim(const RowAttnArgs& a, int D, dim3 grid, hipStream_t stream) {
+static int launch_dim(const RowAttnArgs& a, int D, hipStream_t stream) {
   switch (D) {
-    case 32: launch_typed<T, 32>(a, grid, stream); break;
-    case 64: launch_typed<T, 64>(a, grid, stream); break;
-    case 128: launch_typed<T, 128>(a, grid, stream); break;
-    case 256: launch_typed<T, 256>(a, grid, stream); break;
+    case 32: launch_typed<T, 32>(a, stream); break;
+    case 64: launch_typed<T, 64>(a, stream); break;
+    case 128: launch_typed<T, 128>(a, stream); break;
+    case 256: launch_typed<T, 256>(a, stream); break;
     default: return fail(HS_EUNSUPPORTED, "unsupported head_dim " + std::to_string(D));
   }
   return check_launch("paged attention");
@@ -308,16 +356,16 @@ static int launch_dim(const RowAttnArgs& a, int D, dim3 grid, hipStream_t stream
 // Launch the partition kernel (+ merge when P > 1).  Arguments are validated
 // by the caller.
 int launch_row_attn(const RowAttnArgs& a, int kv_dtype, int D, hipStream_t stream) {
-  const int64_t gx = (int64_t)a.rows * a.P * ((a.H + kDecodeWaves - 1) / kDecodeWaves);
+  const int G = row_attn_heads_per_wave(a.H, a.Hkv);
+  const int64_t gx = (int64_t)a.rows * a.P * ((a.H / G + kDecodeWaves - 1) / kDecodeWaves);
   if (gx <= 0) return HS_OK;
   if (gx > 0x7fffffffLL)
     return fail(HS_EUNSUPPORTED, "grid too large: rows * partitions * head groups = " +
                                      std::to_string(gx));
-  const dim3 grid((unsigned)gx);
   switch (kv_dtype) {
-    case HS_DTYPE_F32: return launch_dim<float>(a, D, grid, stream);
-    case HS_DTYPE_F16: return launch_dim<_Float16>(a, D, grid, stream);
-    case HS_DTYPE_BF16: return launch_dim<Bf16>(a, D, grid, stream);
+    case HS_DTYPE_F32: return launch_dim<float>(a, D, stream);
+    case HS_DTYPE_F16: return launch_dim<_Float16>(a, D, stream);
+    case HS_DTYPE_BF16: return launch_dim<Bf16>(a, D, stream);
     default: return fail(HS_EINVAL, "unknown kv dtype code " + std::to_string(kv_dtype));
   }
 }

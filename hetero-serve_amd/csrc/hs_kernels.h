@@ -35,6 +35,9 @@ void profile_end(hipStream_t stream);
 
 int launch_row_attn(const RowAttnArgs& a, int kv_dtype, int D, hipStream_t stream);
 
+// Query heads one decode wave serves (GQA packing): 1, 2, 4 or 8.
+int row_attn_heads_per_wave(int H, int Hkv);
+
 int launch_page_copy(const void* pool, void* buf, bool unpack, int L, int NB, int64_t page_bytes,
                      const int64_t* ids, int n, hipStream_t stream);
 

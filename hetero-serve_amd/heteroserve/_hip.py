@@ -22,7 +22,7 @@ import threading
 from pathlib import Path
 from typing import Optional
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
 
 _lock = threading.Lock()
@@ -40,7 +40,7 @@ _SIGNATURES = {
     "hs_profile_next_launch": (_c_int, [_c_vp, _c_vp]),
     "hs_device_cu_count": (_c_int, [_c_int]),
     "hs_choose_num_splits": (_c_i64, [_c_i64, _c_i64, _c_i64]),
-    "hs_decode_workspace_bytes": (_c_size, [_c_int] * 7),
+    "hs_decode_workspace_bytes": (_c_size, [_c_int] * 8),
     "hs_decode": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_vp, _c_vp, _c_vp,
                            _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float,
                            _c_int, _c_int, _c_vp, _c_size, _c_vp]),
@@ -241,7 +241,7 @@ def decode(q, k_cache, v_cache, block_tables, context_lens, scale: float,
     out = torch.empty((B, H, D), dtype=torch.float32, device=q.device)
     if B == 0:
         return out
-    ws_bytes = L.hs_decode_workspace_bytes(B, H, D, BS, max(MB, 1), int(num_splits),
+    ws_bytes = L.hs_decode_workspace_bytes(B, H, Hkv, D, BS, max(MB, 1), int(num_splits),
                                            int(partition_tokens))
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes else None
     with _DeviceGuard(q.device):

@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define HS_ABI_VERSION 1
+#define HS_ABI_VERSION 2
 
 /* KV element type codes (the pool dtype). */
 #define HS_DTYPE_F32 0
@@ -83,9 +83,10 @@ int64_t hs_choose_num_splits(int64_t num_seqs, int64_t num_heads, int64_t max_co
 
 /*
  * Workspace bytes hs_decode needs for these sizes (0 when it needs none).
- * num_splits and partition_tokens as for hs_decode.
+ * num_splits and partition_tokens as for hs_decode; Hkv because the default
+ * partition size depends on the GQA group (version 2 of the ABI added it).
  */
-size_t hs_decode_workspace_bytes(int B, int H, int D, int BS, int MB, int num_splits,
+size_t hs_decode_workspace_bytes(int B, int H, int Hkv, int D, int BS, int MB, int num_splits,
                                  int partition_tokens);
 
 /*

@@ -40,7 +40,7 @@ def test_header_declarations_are_bound_by_the_loader():
 def test_library_exports_every_declared_symbol(lib):
     for name in _declared_functions():
         assert hasattr(lib, name), name
-    assert lib.hs_abi_version() == 1
+    assert lib.hs_abi_version() == 2
     assert lib.hs_last_error() == b""
 
 
@@ -61,13 +61,13 @@ def test_argument_errors_need_no_device(lib):
                        0.1, 0, 0, None, 0, None)
     assert rc == -1 and b"dtype" in lib.hs_last_error()
     # partitioned decode needs a workspace
-    need = lib.hs_decode_workspace_bytes(2, 4, 64, 16, 64, 0, 0)
+    need = lib.hs_decode_workspace_bytes(2, 4, 4, 64, 16, 64, 0, 0)
     assert need > 0
     rc = lib.hs_decode(fake, fake, fake, 1, 8, fake, fake, fake, 2, 4, 4, 64, 16, 64,
                        0.1, 0, 0, None, 0, None)
     assert rc == -4 and b"workspace" in lib.hs_last_error()
-    assert lib.hs_decode_workspace_bytes(2, 4, 64, 16, 64, 1, 0) == 0      # one pass
-    assert lib.hs_decode_workspace_bytes(2, 4, 64, 16, 64, 0, 24) == 0     # bad partition
+    assert lib.hs_decode_workspace_bytes(2, 4, 4, 64, 16, 64, 1, 0) == 0      # one pass
+    assert lib.hs_decode_workspace_bytes(2, 4, 4, 64, 16, 64, 0, 24) == 0     # bad partition
     rc = lib.hs_prefill(fake, fake, fake, 0, 8, fake, fake, fake, 1, 4, 4, 4, 64, 16, 2,
                         0.1, 1, None)
     assert rc == -2 and b"fp16 or bf16" in lib.hs_last_error()
@@ -100,13 +100,24 @@ def test_argument_errors_need_no_device(lib):
 
 def test_workspace_size_formula(lib):
     """hs_decode's workspace: (rows * H * P * D) floats, padded to 256 bytes,
-    then rows * H * P (max, sum) pairs; P = ceil(MB * BS / partition)."""
+    then rows * H * P (max, sum) pairs; P = ceil(MB * BS / partition).  The
+    default partition is 512 tokens, min(512, 1024 / G) when one wave serves
+    G query heads of a GQA group (G = 1, 2, 4, 8, the largest dividing H / Hkv)."""
     B, H, D, BS, MB = 3, 5, 128, 16, 100
-    for part, P in ((256, 7), (512, 4), (16, 100)):
+
+    def ws(P):
         acc = (B * H * P * D * 4 + 255) // 256 * 256
-        assert lib.hs_decode_workspace_bytes(B, H, D, BS, MB, 0, part) == acc + B * H * P * 8
-    acc = (B * H * 9 * D * 4 + 255) // 256 * 256
-    assert lib.hs_decode_workspace_bytes(B, H, D, BS, MB, 9, 0) == acc + B * H * 9 * 8
+        return acc + B * H * P * 8
+
+    for part, P in ((256, 7), (512, 4), (16, 100)):
+        assert lib.hs_decode_workspace_bytes(B, H, H, D, BS, MB, 0, part) == ws(P)
+    assert lib.hs_decode_workspace_bytes(B, H, H, D, BS, MB, 9, 0) == ws(9)
+    H = 32
+    for Hkv, part in ((32, 512), (16, 512), (8, 256), (4, 128), (1, 128), (2, 128)):
+        P = -(-(MB * BS) // part)
+        acc = (B * H * P * D * 4 + 255) // 256 * 256
+        assert lib.hs_decode_workspace_bytes(B, H, Hkv, D, BS, MB, 0, 0) == acc + B * H * P * 8
+    assert lib.hs_decode_workspace_bytes(B, H, 5, D, BS, MB, 0, 0) == 0   # H % Hkv != 0
 
 
 def test_module_state_without_a_device(monkeypatch):

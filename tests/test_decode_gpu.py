@@ -173,14 +173,20 @@ def test_decode_block_sizes(bs):
     assert _maxerr(m3.paged_attention_v3(q, kp, vp, bt, ctx, 0.125, 3), want) <= 2e-3
 
 
-@pytest.mark.parametrize("H,Hkv", [(8, 2), (8, 1), (12, 4), (6, 6), (5, 5)])
+@pytest.mark.parametrize("H,Hkv", [(8, 2), (8, 1), (12, 4), (6, 6), (5, 5), (32, 16), (32, 4),
+                                   (24, 2), (16, 1), (64, 8)])
 def test_decode_gqa_and_odd_head_counts(H, Hkv):
-    """GQA/MQA head mapping, and head counts that do not fill a 4-wave workgroup."""
-    m1, _, _ = _mods()
-    pool, q, bt, ctx = _random_case([40, 333], H, Hkv, 128, 16, torch.bfloat16, seed=H * 10 + Hkv)
+    """GQA/MQA head mapping (one wave serves 1, 2, 4 or 8 query heads of a
+    group), and head counts that do not fill a workgroup, on every entry point."""
+    m1, m2, m3 = _mods()
+    pool, q, bt, ctx = _random_case([40, 333, 1029], H, Hkv, 128, 16, torch.bfloat16,
+                                    seed=H * 10 + Hkv)
     kp, vp = pool[0, 0], pool[0, 1]
     want = _oracle(q, kp, vp, bt, ctx, 128 ** -0.5)
     assert _maxerr(m1.paged_attention(q, kp, vp, bt, ctx, 128 ** -0.5), want) <= 2e-3
+    assert _maxerr(m2.paged_attention_v2(q, kp, vp, bt, ctx, 128 ** -0.5), want) <= 2e-3
+    for n in (0, 3, 16):
+        assert _maxerr(m3.paged_attention_v3(q, kp, vp, bt, ctx, 128 ** -0.5, n), want) <= 2e-3
 
 
 def test_zero_context_gives_zero_rows():
