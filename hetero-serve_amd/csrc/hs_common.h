@@ -84,6 +84,14 @@ __device__ inline uint4 load16_stream(const void* p) {
   return make_uint4(x[0], x[1], x[2], x[3]);
 }
 
+// 16-byte store with the non-temporal hint, for data written once and not
+// read back by this kernel.
+__device__ inline void store16_stream(void* p, const uint4& v) {
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 x = {v.x, v.y, v.z, v.w};
+  __builtin_nontemporal_store(x, reinterpret_cast<u32x4*>(p));
+}
+
 // ---------------------------------------------------------------------------
 // Wave reductions
 // ---------------------------------------------------------------------------

