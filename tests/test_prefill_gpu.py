@@ -210,3 +210,30 @@ def test_prefill_configs(name):
             want = decode_one(case.q[cu[b] + r].cpu(), kb, vb, local, pos + 1, case.scale)
             err = _maxerr(got[cu[b] + r], want)
             assert err <= 2e-3, f"{name} seq {b} row {r}: err {err:.2e}"
+
+
+@pytest.mark.parametrize("n_seq,H,Hkv", [(300, 4, 2), (256, 12, 4), (9, 12, 3)])
+def test_mfma_dispatch_orders(n_seq, H, Hkv):
+    """The matrix-core kernel's two dispatch orders: longest-first ranking of
+    up to 256 sequences (every XCD taking heads h % 8, here with 12 heads, so
+    XCDs hold 1 or 2 heads) and the (sequence, head)-major order above 256
+    sequences; ragged chunks against the per-sequence oracle."""
+    from heteroserve.model import paged_attn_prefill as pf
+    from hsbench.cases import build_prefill
+
+    _wmma()
+    rng = np.random.default_rng(n_seq + H)
+    prefix = rng.integers(0, 200, size=n_seq)
+    chunk = rng.integers(1, 60 if n_seq > 100 else 400, size=n_seq)
+    need = int(sum(-(-int(p + s) // 16) for p, s in zip(prefix, chunk)))
+    case = build_prefill("t", prefix, chunk, H, Hkv, 64, need + 16, torch.bfloat16, DEV,
+                         seed=n_seq)
+    got = pf.paged_attention_prefill_varlen(case.q, case.cu_seqlens, int(case.q_lens.max()),
+                                            case.k_cache, case.v_cache, case.block_tables,
+                                            case.context_lens, case.scale, use_mfma=True)
+    cu = case.cu_seqlens.cpu().numpy()
+    for b in sorted({0, n_seq - 1, *rng.integers(0, n_seq, size=12).tolist()}):
+        qb = case.q[cu[b]:cu[b + 1]]
+        want = prefill_one(qb.cpu(), case.k_cache.cpu(), case.v_cache.cpu(),
+                           case.block_tables[b].cpu(), int(case.ctx[b]), case.scale)
+        assert _maxerr(got[cu[b]:cu[b + 1]], want) <= 2e-3, b
