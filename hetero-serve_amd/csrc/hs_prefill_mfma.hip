@@ -6,18 +6,16 @@
 // query i of a chunk of S_b rows sits at position ctx_b - S_b + i and attends
 // to keys [0, that position]; rows at negative positions are zero.
 //
-// Work decomposition.  A workgroup owns 128 query rows (4 waves x 32 rows) of
-// one (sequence, head) and walks that head's keys in tiles of 64 (four
-// 16-token pages), staging each K/V tile in LDS once for all four waves.  The
-// LDS tiles are double-buffered with one barrier per tile, and the next
-// tile's global loads are in flight while the current one is consumed.  The
-// kernel is held to two waves per SIMD (<= 256 registers), so one wave's
-// softmax overlaps the other's MFMAs; measured on C4 this beat 64 rows per
-// wave at one wave per SIMD by 1.8x, even though each LDS fragment then feeds
-// one MFMA instead of two.  Two 64-key tiles take 70 KiB of LDS, so two
-// workgroups share a CU and one's pipeline fill overlaps the other's compute
-// (measured: 8-wave workgroups with 128-key tiles, one per CU, were 20-30%
-// slower on every prefill shape tried).
+// Work decomposition.  A workgroup owns 256 query rows (8 waves x 32 rows; 4
+// waves at head dim 32) of one (sequence, head) and walks that head's keys in
+// tiles of 64 (four 16-token pages), staging each K/V tile in LDS once for all
+// of its waves.  The LDS tiles are double-buffered with one barrier per tile,
+// and the global loads of later tiles are in flight while the current one is
+// consumed.  The kernel is held to two waves per SIMD (<= 256 registers), one
+// workgroup per CU: a wave's softmax (VALU) then runs while the other wave of
+// its SIMD issues MFMAs, which measured faster than 64 rows per wave at one
+// wave per SIMD, even though each LDS fragment then feeds one MFMA instead of
+// two.
 // Scores are computed transposed, S^T = K . Q^T, with v_mfma_f32_32x32x16_f16:
 // K rows are the A operand (read from LDS), Q^T the B operand (held in
 // registers for the whole walk).  The accumulator then has one query per
