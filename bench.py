@@ -51,6 +51,8 @@ def log(*a) -> None:
 # calibrated on a 1 GiB copy) for the default workload; summarised in the
 # committed profile below, whose table this reads.
 TRAFFIC_PROFILE = ROOT / "profiles" / "decode_C2_prefill_C4_pack_C5.md"
+# The headline leg's dominant kernel, as rocprofv3 names it.
+DECODE_KERNEL = "hs::row_attn_part_kernel<hs::Bf16, 128, true, 1>"
 
 
 def profiled_traffic(kernel: str):
@@ -406,7 +408,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(dec["kernel_gbs"] / HBM_PEAK_GBS, 4),
-            "traffic": profiled_traffic("hs::row_attn_part_kernel<hs::Bf16, 128, true>")
+            "traffic": profiled_traffic(DECODE_KERNEL)
             if args.config == "C2" and not args.partition else None,
             "traffic_source": TRAFFIC_PROFILE.name,
             "algorithmic_bytes": dec["bytes"],
