@@ -321,7 +321,9 @@ __device__ inline float16x qk_block(const PrefillTileLds<D>& t, int kb, const ha
 struct RankScratch {
   int keys[kMaxRanked];      // keys walked by each sequence's last tile
   int tiles[kMaxRanked];     // query tiles of each sequence
-  int order[kMaxRanked];     // sequences by decreasing keys
+  int ctx[kMaxRanked];       // context length, first row and rows of each
+  int row0[kMaxRanked];      // sequence, kept so that the chosen one's need
+  int rows[kMaxRanked];      // no second trip to memory
   int b, qt;
 };
 
@@ -339,32 +341,28 @@ __device__ inline bool ranked_tile(const PrefillArgs& a, RankScratch& rs, int& b
   const int tid = threadIdx.x;
   if (tid < a.B) {
     const int rows = seq_rows(a, tid);
-    rs.keys[tid] = rows > 0 ? min(a.MB * 16, a.ctx[tid]) : -1;
+    const int ctx = a.ctx[tid];
+    rs.keys[tid] = rows > 0 ? min(a.MB * 16, ctx) : -1;
     rs.tiles[tid] = (rows + kBM - 1) / kBM;
+    rs.ctx[tid] = ctx;
+    rs.row0[tid] = a.cu_q ? a.cu_q[tid] : tid * a.S;
+    rs.rows[tid] = rows;
   }
   if (tid == 0) rs.b = -1;
   __syncthreads();
+  // Sequence tid's first slot in the ranked layout is the tile count of the
+  // sequences ranked before it; the thread whose range holds slot r claims it.
   if (tid < a.B) {
     const int k = rs.keys[tid];
-    int rank = 0;
+    int start = 0;
     for (int q = 0; q < a.B; ++q) {
       const int kq = rs.keys[q];
-      rank += (kq > k) | ((kq == k) & (q < tid));
+      start += ((kq > k) | ((kq == k) & (q < tid))) ? rs.tiles[q] : 0;
     }
-    rs.order[rank] = tid;
-  }
-  __syncthreads();
-  if (tid == 0) {
-    int start = 0;
-    for (int i = 0; i < a.B; ++i) {
-      const int bb = rs.order[i];
-      const int n = rs.tiles[bb];
-      if (r < start + n) {
-        rs.b = bb;
-        rs.qt = n - 1 - (r - start);
-        break;
-      }
-      start += n;
+    const int n = rs.tiles[tid];
+    if (r >= start && r < start + n) {
+      rs.b = tid;
+      rs.qt = n - 1 - (r - start);
     }
   }
   __syncthreads();
@@ -385,10 +383,13 @@ void prefill_mfma_kernel(PrefillArgs a) {
   __shared__ PrefillTileLds<D> lds[2];
 
   // ---- which (sequence, head, query tile) -------------------------------
-  int b, h, qt;
+  int b, h, qt, row0, S_b, ctx_b;
   if (a.ranked) {
     __shared__ RankScratch rank_scratch;
     if (!ranked_tile<kBM>(a, rank_scratch, b, h, qt)) return;
+    row0 = rank_scratch.row0[b];
+    S_b = rank_scratch.rows[b];
+    ctx_b = rank_scratch.ctx[b];
   } else {
     // all query tiles of one (sequence, head) on one XCD, heaviest first
     const int xcd = blockIdx.x % kXcds;
@@ -398,14 +399,14 @@ void prefill_mfma_kernel(PrefillArgs a) {
     qt = a.n_qt - 1 - slot % a.n_qt;
     b = pair / a.H;
     h = pair - b * a.H;
-  }
-  int row0, S_b;
-  if (a.cu_q) {
-    row0 = a.cu_q[b];
-    S_b = a.cu_q[b + 1] - row0;
-  } else {
-    row0 = b * a.S;
-    S_b = a.S;
+    if (a.cu_q) {
+      row0 = a.cu_q[b];
+      S_b = a.cu_q[b + 1] - row0;
+    } else {
+      row0 = b * a.S;
+      S_b = a.S;
+    }
+    ctx_b = a.ctx[b];
   }
   if (qt * kBM >= S_b) return;
 
@@ -415,7 +416,7 @@ void prefill_mfma_kernel(PrefillArgs a) {
   const int hh = lane >> 5;         // lane half
   const int kvh = h / (a.H / a.Hkv);
   const int cap = a.MB * 16;        // keys the block table can address
-  const int base_pos = a.ctx[b] - S_b;   // position of row 0 of the chunk
+  const int base_pos = ctx_b - S_b;     // position of row 0 of the chunk
   const int32_t* bt = a.bt + (int64_t)b * a.MB;
 
   // This lane's query row and its inclusive key limit (-1: padding row).
@@ -430,23 +431,9 @@ void prefill_mfma_kernel(PrefillArgs a) {
                                             cap - 1)
                                       : -1;
 
-  // ---- Q^T fragments: lane (j, hh) holds q[row][16c + 8hh .. +7] ---------
+  // Q^T fragments: lane (j, hh) holds q[row][16c + 8hh .. +7] (loaded in the
+  // prologue below, beside the first tile's loads)
   half8 qf[kDC16];
-  {
-    const float* qp = a.q + ((int64_t)(row0 + min(i_row, S_b - 1)) * a.H + h) * D + 8 * hh;
-    const float sc = a.qscale;
-#pragma unroll
-    for (int c = 0; c < kDC16; ++c) {
-      float4 x0 = make_float4(0.f, 0.f, 0.f, 0.f), x1 = x0;
-      if (row_ok) {
-        x0 = *reinterpret_cast<const float4*>(qp + 16 * c);
-        x1 = *reinterpret_cast<const float4*>(qp + 16 * c + 4);
-      }
-      qf[c] = __builtin_bit_cast(
-          half8, make_uint4(pack_f16(x0.x * sc, x0.y * sc), pack_f16(x0.z * sc, x0.w * sc),
-                            pack_f16(x1.x * sc, x1.y * sc), pack_f16(x1.z * sc, x1.w * sc)));
-    }
-  }
 
   float16x o[kDB];
 #pragma unroll
@@ -476,19 +463,41 @@ void prefill_mfma_kernel(PrefillArgs a) {
     // the compiler counts outstanding loads exactly and waits only for the tile
     // it is about to store (a load issued under a condition makes it wait for
     // all of them).  The last tile pairs run a tail copy of the step that loads
-    // only what is still needed.  The prologue's loads are unconditional too:
-    // ids are clamped to the table and a tile past the end reads a valid page.
-    if (n_kt > 0) {
-      if constexpr (kProd) {
-        pr.template fetch_ids<0>(a, bt, 0);
-        pr.template fetch_ids<1>(a, bt, 1);
-        pr.template load_tile<T, 0>(a, rg);
-        pr.template store_tile<T>(lds[0], rg);
-        pr.template fetch_ids<0>(a, bt, 2);
-        pr.template load_tile<T, 1>(a, rg);
-      }
-      __syncthreads();
+    // only what is still needed.
+    // The prologue is ordered so that its memory round trips overlap: block
+    // ids of tiles 0 and 1, then Q, then tile 0's K/V (waiting for the ids
+    // only), then Q's conversion, tile 0's LDS store and tile 1's loads.  Its
+    // loads are unconditional too: ids are clamped to the table, so a tile past
+    // the end reads a valid page, and a padding row reads the chunk's last row
+    // (scaled to zero).
+    if constexpr (kProd) {
+      pr.template fetch_ids<0>(a, bt, 0);
+      pr.template fetch_ids<1>(a, bt, 1);
     }
+    {
+      float4 x[2 * kDC16];
+      const float* qp = a.q + ((int64_t)(row0 + min(i_row, S_b - 1)) * a.H + h) * D + 8 * hh;
+#pragma unroll
+      for (int c = 0; c < kDC16; ++c) {
+        x[2 * c] = *reinterpret_cast<const float4*>(qp + 16 * c);
+        x[2 * c + 1] = *reinterpret_cast<const float4*>(qp + 16 * c + 4);
+      }
+      if constexpr (kProd) pr.template load_tile<T, 0>(a, rg);
+      const float sc = row_ok ? a.qscale : 0.0f;   // padding rows: q = 0
+#pragma unroll
+      for (int c = 0; c < kDC16; ++c) {
+        const float4 x0 = x[2 * c], x1 = x[2 * c + 1];
+        qf[c] = __builtin_bit_cast(
+            half8, make_uint4(pack_f16(x0.x * sc, x0.y * sc), pack_f16(x0.z * sc, x0.w * sc),
+                              pack_f16(x1.x * sc, x1.y * sc), pack_f16(x1.z * sc, x1.w * sc)));
+      }
+    }
+    if constexpr (kProd) {
+      pr.template store_tile<T>(lds[0], rg);
+      pr.template fetch_ids<0>(a, bt, 2);
+      pr.template load_tile<T, 1>(a, rg);
+    }
+    __syncthreads();
 
     // One tile: consume tile kt from buffer kSet ^ 1, write tile kt+1 from the
     // register set into buffer kSet, refill the set with tile kt+2 (block ids of
