@@ -58,6 +58,7 @@ COMPILE_FLAGS = [
 # instruction count by ~45% (measured on the generated gfx950 code).
 PER_FILE_FLAGS = {
     "hs_prefill_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=true"],
+    "hs_decode_gqa.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=true"],
 }
 
 

@@ -87,8 +87,14 @@ struct DecodePlan {
 
 // Default partition: 512 tokens, shorter when a wave serves G > 2 query
 // heads of a GQA group (fewer waves, each doing G times the work per token):
-// measured on C2's geometry with 8 and 4 KV heads, 256 and 128 tokens.
+// measured on C2's geometry with 8 and 4 KV heads, 256 and 128 tokens.  With
+// 8 or more query heads per KV head and at most 2 waves' worth of heads per
+// row (matrix-core path, 32 heads a wave), 512 again: there the merge of many
+// short partitions cost more than the waves it adds (MQA with 32 heads on
+// C2's geometry: 65 us at 512 tokens, 90 us at 128).
 static int default_partition(int H, int Hkv) {
+  const int G = H / Hkv;
+  if (G >= 8 && Hkv * ((G + 31) / 32) <= 2) return kDefaultPartition;
   return std::min(kDefaultPartition, 1024 / row_attn_heads_per_wave(H, Hkv));
 }
 

@@ -29,49 +29,6 @@
 
 namespace hs {
 
-// Sequence of a row and the end of its key range (exclusive).  Returns false
-// for grid rows past the last real row (ragged batches size the grid by the
-// longest sequence).
-__device__ inline bool row_geometry(const RowAttnArgs& a, int row, int& b, int& end) {
-  int s, rows_b;
-  if (a.cu_q) {
-    if (row >= a.cu_q[a.B]) return false;
-    int lo = 0, hi = a.B;  // find b with cu_q[b] <= row < cu_q[b+1]
-    while (hi - lo > 1) {
-      const int mid = (lo + hi) >> 1;
-      if (a.cu_q[mid] <= row) lo = mid; else hi = mid;
-    }
-    b = lo;
-    s = row - a.cu_q[b];
-    rows_b = a.cu_q[b + 1] - a.cu_q[b];
-  } else {
-    b = row / a.S;
-    s = row - b * a.S;
-    rows_b = a.S;
-  }
-  const int64_t cap = (int64_t)a.MB * a.BS;
-  const int64_t e = (int64_t)a.ctx[b] - rows_b + s + 1;
-  end = (int)(e < cap ? e : cap);
-  return true;
-}
-
-// Key range [lo, hi) of partition p; returns false when it is empty.
-__device__ inline bool partition_range(const RowAttnArgs& a, int end, int p, int& lo, int& hi,
-                                       int& nparts) {
-  if (end <= 0) {
-    nparts = 0;
-    return false;
-  }
-  int chunk;
-  if (a.mode == 0) chunk = end;
-  else if (a.mode == 1) chunk = a.part_tokens;
-  else chunk = (end + a.splits - 1) / a.splits;
-  nparts = (end + chunk - 1) / chunk;
-  lo = p * chunk;
-  hi = min(lo + chunk, end);
-  return p < nparts;
-}
-
 constexpr int kDecodeWaves = 2;  // waves per workgroup
 
 // One wave = G query heads of one KV group for one (row, partition): each
@@ -313,6 +270,17 @@ int row_attn_heads_per_wave(int H, int Hkv) {
   return g;
 }
 
+static void launch_merge(const RowAttnArgs& a, int D, hipStream_t stream) {
+  const int64_t waves = (int64_t)a.rows * a.H;
+  const dim3 grid((unsigned)((waves + 3) / 4)), block(256);
+  switch (D) {
+    case 32: hipLaunchKernelGGL((row_attn_merge_kernel<32>), grid, block, 0, stream, a); break;
+    case 64: hipLaunchKernelGGL((row_attn_merge_kernel<64>), grid, block, 0, stream, a); break;
+    case 128: hipLaunchKernelGGL((row_attn_merge_kernel<128>), grid, block, 0, stream, a); break;
+    default: hipLaunchKernelGGL((row_attn_merge_kernel<256>), grid, block, 0, stream, a); break;
+  }
+}
+
 template <typename T, int D, int G>
 static void launch_part(const RowAttnArgs& a, hipStream_t stream) {
   const int tpl = 64 / (D / Elem<T>::kVec);
@@ -334,11 +302,7 @@ static void launch_typed(const RowAttnArgs& a, hipStream_t stream) {
     default: launch_part<T, D, 1>(a, stream); break;
   }
   profile_end(stream);
-  if (a.P > 1) {
-    const int64_t waves = (int64_t)a.rows * a.H;
-    hipLaunchKernelGGL((row_attn_merge_kernel<D>), dim3((unsigned)((waves + 3) / 4)), dim3(256),
-                       0, stream, a);
-  }
+  if (a.P > 1) launch_merge(a, D, stream);
 }
 
 template <typename T>
@@ -354,8 +318,21 @@ static int launch_dim(const RowAttnArgs& a, int D, hipStream_t stream) {
 }
 
 // Launch the partition kernel (+ merge when P > 1).  Arguments are validated
-// by the caller.
+// by the caller.  Grouped-query calls that the matrix-core kernel serves go
+// there (hs_decode_gqa.hip); the rest run the VALU kernel above.
 int launch_row_attn(const RowAttnArgs& a, int kv_dtype, int D, hipStream_t stream) {
+  if (gqa_mfma_applies(a, kv_dtype, D)) {
+    const int64_t gx = gqa_mfma_grid(a);
+    if (gx <= 0) return HS_OK;
+    if (gx > 0x7fffffffLL)
+      return fail(HS_EUNSUPPORTED, "grid too large: rows * partitions * head groups = " +
+                                       std::to_string(gx));
+    profile_begin(stream);
+    launch_gqa_mfma_part(a, kv_dtype, D, stream);
+    profile_end(stream);
+    if (a.P > 1) launch_merge(a, D, stream);
+    return check_launch("paged attention");
+  }
   const int G = row_attn_heads_per_wave(a.H, a.Hkv);
   const int64_t gx = (int64_t)a.rows * a.P * ((a.H / G + kDecodeWaves - 1) / kDecodeWaves);
   if (gx <= 0) return HS_OK;

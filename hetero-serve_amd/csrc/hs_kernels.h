@@ -28,12 +28,62 @@ struct RowAttnArgs {
   float qscale;           // scale * log2(e)
 };
 
+// Sequence of a row and the end of its key range (exclusive).  Returns false
+// for grid rows past the last real row (ragged batches size the grid by the
+// longest sequence).
+__device__ inline bool row_geometry(const RowAttnArgs& a, int row, int& b, int& end) {
+  int s, rows_b;
+  if (a.cu_q) {
+    if (row >= a.cu_q[a.B]) return false;
+    int lo = 0, hi = a.B;  // find b with cu_q[b] <= row < cu_q[b+1]
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (a.cu_q[mid] <= row) lo = mid; else hi = mid;
+    }
+    b = lo;
+    s = row - a.cu_q[b];
+    rows_b = a.cu_q[b + 1] - a.cu_q[b];
+  } else {
+    b = row / a.S;
+    s = row - b * a.S;
+    rows_b = a.S;
+  }
+  const int64_t cap = (int64_t)a.MB * a.BS;
+  const int64_t e = (int64_t)a.ctx[b] - rows_b + s + 1;
+  end = (int)(e < cap ? e : cap);
+  return true;
+}
+
+// Key range [lo, hi) of partition p; returns false when it is empty.
+__device__ inline bool partition_range(const RowAttnArgs& a, int end, int p, int& lo, int& hi,
+                                       int& nparts) {
+  if (end <= 0) {
+    nparts = 0;
+    return false;
+  }
+  int chunk;
+  if (a.mode == 0) chunk = end;
+  else if (a.mode == 1) chunk = a.part_tokens;
+  else chunk = (end + a.splits - 1) / a.splits;
+  nparts = (end + chunk - 1) / chunk;
+  lo = p * chunk;
+  hi = min(lo + chunk, end);
+  return p < nparts;
+}
+
 // Measurement hook of hs_profile_next_launch: bracket the main kernel of the
 // current call with the caller's events (no-ops when none are pending).
 void profile_begin(hipStream_t stream);
 void profile_end(hipStream_t stream);
 
 int launch_row_attn(const RowAttnArgs& a, int kv_dtype, int D, hipStream_t stream);
+
+// Grouped-query partition kernel on the matrix cores (hs_decode_gqa.hip):
+// whether it serves this call, its grid size, and its launch (the merge of
+// its partition states is the VALU path's).
+bool gqa_mfma_applies(const RowAttnArgs& a, int kv_dtype, int D);
+int64_t gqa_mfma_grid(const RowAttnArgs& a);
+void launch_gqa_mfma_part(const RowAttnArgs& a, int kv_dtype, int D, hipStream_t stream);
 
 // Query heads one decode wave serves (GQA packing): 1, 2, 4 or 8.
 int row_attn_heads_per_wave(int H, int Hkv);

@@ -47,6 +47,7 @@
 // head) pairs alternate XCDs.  The tiles of one head then share its K/V
 // through that XCD's L2.
 #include "hs_kernels.h"
+#include "hs_mfma.h"
 
 #include <type_traits>
 
@@ -54,10 +55,7 @@ namespace hs {
 
 namespace {
 
-typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-typedef _Float16 half2x __attribute__((ext_vector_type(2)));
-typedef float float16x __attribute__((ext_vector_type(16)));
-typedef float float2x __attribute__((ext_vector_type(2)));
+using namespace mfma;
 
 constexpr int kRowsPerWave = 32;             // one 32-row MFMA tile per wave
 constexpr int kBN = 64;                      // keys per LDS tile (four pages), a multiple of 32
@@ -98,73 +96,6 @@ struct PrefillTileLds {
   _Float16 k[kBN][D + kKPad];       // K tile, row r holds key swap23(r)
   _Float16 vt[D][kBN + kVPad];      // V tile transposed
 };
-
-__device__ inline int swap_bits23(int r) {
-  return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1);
-}
-
-__device__ inline uint32_t pack_f16(float a, float b) {
-  const half2x h = __builtin_convertvector((float2x){a, b}, half2x);  // v_cvt_pk_f16_f32, RNE
-  return __builtin_bit_cast(uint32_t, h);
-}
-
-// Element e (0..7) of 8 packed 16-bit KV values, widened to fp32 (exact).
-template <typename T>
-__device__ inline float elem_f32(const uint4& w, int e);
-
-template <>
-__device__ inline float elem_f32<Bf16>(const uint4& w, int e) {
-  const uint32_t d = e < 2 ? w.x : e < 4 ? w.y : e < 6 ? w.z : w.w;
-  return __uint_as_float((e & 1) ? (d & 0xffff0000u) : (d << 16));
-}
-
-template <>
-__device__ inline float elem_f32<_Float16>(const uint4& w, int e) {
-  const uint32_t d = e < 2 ? w.x : e < 4 ? w.y : e < 6 ? w.z : w.w;
-  const half2x h = __builtin_bit_cast(half2x, d);
-  return (float)h[e & 1];
-}
-
-// 8 KV elements -> 8 fp16.
-template <typename T>
-__device__ inline uint4 to_f16x8(const uint4& w) {
-  return make_uint4(pack_f16(elem_f32<T>(w, 0), elem_f32<T>(w, 1)),
-                    pack_f16(elem_f32<T>(w, 2), elem_f32<T>(w, 3)),
-                    pack_f16(elem_f32<T>(w, 4), elem_f32<T>(w, 5)),
-                    pack_f16(elem_f32<T>(w, 6), elem_f32<T>(w, 7)));
-}
-
-template <>
-__device__ inline uint4 to_f16x8<_Float16>(const uint4& w) {
-  return w;
-}
-
-// Element e of two chunks, as the fp16 pair (x[e], y[e]).
-template <typename T>
-__device__ inline uint32_t pack_col(const uint4& x, const uint4& y, int e) {
-  return pack_f16(elem_f32<T>(x, e), elem_f32<T>(y, e));
-}
-
-template <>
-__device__ inline uint32_t pack_col<_Float16>(const uint4& x, const uint4& y, int e) {
-  const uint32_t xw = e < 2 ? x.x : e < 4 ? x.y : e < 6 ? x.z : x.w;
-  const uint32_t yw = e < 2 ? y.x : e < 4 ? y.y : e < 6 ? y.z : y.w;
-  // v_perm_b32: bytes {x half, y half} of the selected 16-bit lanes
-  return __builtin_amdgcn_perm(yw, xw, (e & 1) ? 0x07060302u : 0x05040100u);
-}
-
-// Both lane halves' values of x: {lanes 0-31, lanes 32-63} seen from each lane.
-__device__ inline float sum_halves(float x) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
-                                                  false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-
-__device__ inline float max_halves(float x) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
-                                                  false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
 
 // The producer: how the first half of a workgroup's waves (256 threads at
 // head dim 128) move one K/V tile from the paged cache through registers

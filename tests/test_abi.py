@@ -102,7 +102,8 @@ def test_workspace_size_formula(lib):
     """hs_decode's workspace: (rows * H * P * D) floats, padded to 256 bytes,
     then rows * H * P (max, sum) pairs; P = ceil(MB * BS / partition).  The
     default partition is 512 tokens, min(512, 1024 / G) when one wave serves
-    G query heads of a GQA group (G = 1, 2, 4, 8, the largest dividing H / Hkv)."""
+    G query heads of a GQA group (G = 1, 2, 4, 8, the largest dividing H / Hkv),
+    and 512 again when H / Hkv >= 8 and Hkv * ceil(H / Hkv / 32) <= 2."""
     B, H, D, BS, MB = 3, 5, 128, 16, 100
 
     def ws(P):
@@ -113,7 +114,12 @@ def test_workspace_size_formula(lib):
         assert lib.hs_decode_workspace_bytes(B, H, H, D, BS, MB, 0, part) == ws(P)
     assert lib.hs_decode_workspace_bytes(B, H, H, D, BS, MB, 9, 0) == ws(9)
     H = 32
-    for Hkv, part in ((32, 512), (16, 512), (8, 256), (4, 128), (1, 128), (2, 128)):
+    for Hkv, part in ((32, 512), (16, 512), (8, 256), (4, 128), (1, 512), (2, 512)):
+        P = -(-(MB * BS) // part)
+        acc = (B * H * P * D * 4 + 255) // 256 * 256
+        assert lib.hs_decode_workspace_bytes(B, H, Hkv, D, BS, MB, 0, 0) == acc + B * H * P * 8
+    H = 96                                     # G = 96: three 32-head waves per KV head
+    for Hkv, part in ((1, 128), (3, 128)):
         P = -(-(MB * BS) // part)
         acc = (B * H * P * D * 4 + 255) // 256 * 256
         assert lib.hs_decode_workspace_bytes(B, H, Hkv, D, BS, MB, 0, 0) == acc + B * H * P * 8

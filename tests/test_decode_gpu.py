@@ -238,6 +238,53 @@ def test_split_invariance_and_partition_sizes():
         assert _maxerr(o, outs[0]) <= 1e-4
 
 
+@pytest.mark.parametrize("H,Hkv,D,dtype", [
+    (32, 8, 128, torch.bfloat16),   # llama3-8b shape (config.py:85-93), G = 4
+    (32, 1, 128, torch.bfloat16),   # MQA: one wave serves all 32 query heads
+    (40, 1, 128, torch.float16),    # G = 40: two head chunks, the second of 8
+    (64, 2, 64, torch.bfloat16),    # G = 32 at head_dim 64
+    (16, 2, 32, torch.float16),     # G = 8 at head_dim 32
+    (12, 3, 128, torch.bfloat16),   # G = 4, 3 KV heads (not a multiple of 4 waves)
+])
+def test_gqa_matrix_core_decode(H, Hkv, D, dtype):
+    """Grouped-query decode on the matrix cores (16-token pages, fixed
+    partitions up to 1024 tokens): every partition length from 16 to 1024
+    tokens vs the oracle (2e-3) and vs the one-pass VALU kernel (v2), on
+    contexts that end inside, at and past page and partition boundaries."""
+    from heteroserve import _hip
+
+    m1, m2, _ = _mods()
+    lens = [1, 15, 16, 17, 33, 100, 511, 512, 513, 1500, 3000]
+    pool, q, bt, ctx = _random_case(lens, H, Hkv, D, 16, dtype, seed=H * 7 + Hkv + D)
+    kp, vp = pool[0, 0], pool[0, 1]
+    scale = D ** -0.5
+    want = _oracle(q, kp, vp, bt, ctx, scale)
+    one_pass = m2.paged_attention_v2(q, kp, vp, bt, ctx, scale)
+    assert _maxerr(one_pass, want) <= 2e-3
+    outs = [m1.paged_attention(q, kp, vp, bt, ctx, scale)]
+    outs += [_hip.decode(q, kp, vp, bt, ctx, scale, 0, partition_tokens=p)
+             for p in (16, 48, 128, 512, 1024)]
+    for o in outs:
+        assert _maxerr(o, want) <= 2e-3
+        assert _maxerr(o, one_pass) <= 2e-3
+
+
+def test_gqa_matrix_core_table_edges():
+    """The matrix-core GQA path reads -1 table entries inside the context as
+    block 0 and clamps ctx to the table, as the VALU path and the torch
+    reference do, and gives zero rows for ctx <= 0."""
+    m1, _, _ = _mods()
+    pool, q, bt, ctx = _random_case([40, 64, 300], 16, 2, 128, 16, torch.bfloat16, seed=13)
+    ctx[0] = 10_000            # table holds 3 blocks = 48 positions
+    bt[1, 2] = -1              # hole inside sequence 1's context
+    ctx[2] = 0
+    kp, vp = pool[0, 0], pool[0, 1]
+    want = _oracle(q, kp, vp, bt, ctx, 0.125)
+    got = m1.paged_attention(q, kp, vp, bt, ctx, 0.125).cpu()
+    assert torch.all(got[2] == 0)
+    assert _maxerr(got[[0, 1]], want[[0, 1]]) <= 2e-3
+
+
 def test_errors_are_raised_with_reference_messages():
     m1, m2, _ = _mods()
     pool, q, bt, ctx = _random_case([10], 4, 4, 64, 16, torch.float16, seed=1)
