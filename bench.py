@@ -121,10 +121,13 @@ def prefill_leg(case, steps: int, warmup: int) -> dict:
     B, MB = case.block_tables.shape
     out = torch.empty((T, H, D), dtype=torch.float32, device=case.q.device)
     stream = torch.cuda.current_stream().cuda_stream
-    args = (case.q.data_ptr(), case.cu_seqlens.data_ptr(), int(case.q_lens.max()),
+    max_rows = int(case.q_lens.max())
+    ws, ws_bytes = _hip._prefill_workspace(lib, B, max_rows, H, D, True, True, case.q.device)
+    args = (case.q.data_ptr(), case.cu_seqlens.data_ptr(), max_rows,
             kc.data_ptr(), vc.data_ptr(), _hip.dtype_code(kc.dtype), NB,
             case.block_tables.data_ptr(), case.context_lens.data_ptr(), out.data_ptr(),
-            B, H, Hkv, D, BS, MB, float(case.scale), 1, stream)
+            B, H, Hkv, D, BS, MB, float(case.scale), 1,
+            ws.data_ptr() if ws is not None else None, ws_bytes, stream)
 
     def step():
         _hip.check(lib.hs_prefill_varlen(*args))
@@ -238,6 +241,108 @@ def kv_write_leg(steps: int, warmup: int) -> dict:
     torch.cuda.empty_cache()
     return dict(step_ms=step_ms, kernel_ms=k_ms, ref_ms=ref_ms, bytes=nbytes, bit_exact=exact,
                 kernel_gbs=nbytes / (k_ms * 1e-3) / 1e9)
+
+
+def c5_step_leg(steps: int, warmup: int) -> dict:
+    """C5 as one serving step on one stream: the prefill chunk's K/V written
+    into its cache (1024 tokens at positions 2048..3071, fp32 slices of a fused
+    QKV output), its causal attention on the matrix cores, the 255 decode
+    tokens' K/V appended at ctx - 1, the decode of those 255 sequences (half
+    of them sharing a 1024-token prefix), and the 4096-block migration pack of
+    the decode pool.  Returns the step time and each part timed alone."""
+    import torch
+
+    from heteroserve import _hip
+    from hsbench import cases
+    from hsbench.timing import Event
+
+    lib = _hip.lib()
+    dev = "cuda:0"
+    stream = torch.cuda.current_stream().cuda_stream
+    dc, pc = cases.c5_decode(dev), cases.c5_prefill(dev)
+    g = torch.Generator(device=dev).manual_seed(44)
+    T, H, D = pc.q.shape
+    kvd = H * D
+    pkc, pvc = pc.k_cache, pc.v_cache
+    pnb, bs, hkv, _ = pkc.shape
+    qkv_p = torch.randn((T, 3 * kvd), generator=g, device=dev)
+    ppos = torch.arange(2048, 2048 + T, dtype=torch.int32, device=dev)
+    pseq = torch.zeros(T, dtype=torch.int32, device=dev)
+    pout = torch.empty((T, H, D), dtype=torch.float32, device=dev)
+    B = dc.q.shape[0]
+    dkc, dvc = dc.k_cache, dc.v_cache
+    dnb = dkc.shape[0]
+    dmb = dc.block_tables.shape[1]
+    qkv_d = torch.randn((B, 3 * kvd), generator=g, device=dev)
+    dpos = (dc.context_lens - 1).to(torch.int32).contiguous()
+    dseq = torch.arange(B, dtype=torch.int32, device=dev)
+    dout = torch.empty((B, H, D), dtype=torch.float32, device=dev)
+    ws_bytes = lib.hs_decode_workspace_bytes(B, H, hkv, D, bs, dmb, 0, 0)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    ids = torch.as_tensor(cases.c5_pack_ids(dnb), dtype=torch.int64, device=dev)
+    pool = dc.pool
+    page = pool[0, 0, 0].numel() * pool.element_size()
+    pack_out = torch.empty((ids.numel(), 1, 2, bs, hkv, D), dtype=pool.dtype, device=dev)
+    f32 = _hip.DTYPE_F32
+    kdt = _hip.dtype_code(dkc.dtype)
+    pws, pws_bytes = _hip._prefill_workspace(lib, 1, T, H, D, True, True, dev)
+    parts = {
+        "kv_write_chunk": lambda: lib.hs_kv_append(
+            pkc.data_ptr(), pvc.data_ptr(), kdt, pnb, bs, hkv, D, pc.block_tables.data_ptr(),
+            pc.block_tables.shape[1], ppos.data_ptr(), pseq.data_ptr(), T,
+            qkv_p[:, kvd:].data_ptr(), qkv_p[:, 2 * kvd:].data_ptr(), f32, qkv_p.stride(0),
+            stream),
+        "prefill": lambda: lib.hs_prefill_varlen(
+            pc.q.data_ptr(), pc.cu_seqlens.data_ptr(), T, pkc.data_ptr(), pvc.data_ptr(), kdt,
+            pnb, pc.block_tables.data_ptr(), pc.context_lens.data_ptr(), pout.data_ptr(), 1, H,
+            hkv, D, bs, pc.block_tables.shape[1], float(pc.scale), 1,
+            pws.data_ptr() if pws is not None else None, pws_bytes, stream),
+        "kv_write_decode": lambda: lib.hs_kv_append(
+            dkc.data_ptr(), dvc.data_ptr(), kdt, dnb, bs, hkv, D, dc.block_tables.data_ptr(), dmb,
+            dpos.data_ptr(), dseq.data_ptr(), B, qkv_d[:, kvd:].data_ptr(),
+            qkv_d[:, 2 * kvd:].data_ptr(), f32, qkv_d.stride(0), stream),
+        "decode": lambda: lib.hs_decode(
+            dc.q.data_ptr(), dkc.data_ptr(), dvc.data_ptr(), kdt, dnb,
+            dc.block_tables.data_ptr(), dc.context_lens.data_ptr(), dout.data_ptr(), B, H, hkv,
+            D, bs, dmb, float(dc.scale), 0, 0, ws.data_ptr(), ws_bytes, stream),
+        "pack": lambda: lib.hs_kv_pack(pool.data_ptr(), 1, dnb, page, ids.data_ptr(),
+                                       ids.numel(), pack_out.data_ptr(), stream),
+    }
+
+    def timed(fns) -> float:
+        for _ in range(warmup):
+            for f in fns:
+                _hip.check(f())
+        e0, e1 = Event(), Event()
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for _ in range(steps):
+            for f in fns:
+                _hip.check(f())
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_ms(e1) / steps
+
+    step_ms = timed(list(parts.values()))
+    part_ms = {k: timed([f]) for k, f in parts.items()}
+    work = {
+        "kv_write_chunk": ("GB/s", 2 * T * kvd * (4 + 2) / 1e9),
+        "prefill": ("TFLOP/s", pc.prefill_flops() / 1e12),
+        "kv_write_decode": ("GB/s", 2 * B * kvd * (4 + 2) / 1e9),
+        "decode": ("GB/s", dc.unique_decode_bytes() / 1e9),
+        "pack": ("GB/s", 2 * pack_out.numel() * pack_out.element_size() / 1e9),
+    }
+    peak = {"GB/s": HBM_PEAK_GBS, "TFLOP/s": MFMA_F16_PEAK_TFLOPS}
+    out = {"us_per_step": round(step_ms * 1e3, 2), "parts": {}}
+    for k, ms in part_ms.items():
+        unit, amount = work[k]
+        rate = amount / (ms * 1e-3)
+        out["parts"][k] = {"us": round(ms * 1e3, 2), unit: round(rate, 1),
+                           "frac": round(rate / peak[unit], 4)}
+    out["parts"]["decode"]["basis"] = "unique K/V bytes (shared prefix counted once)"
+    del dc, pc, pool, pack_out, qkv_p, qkv_d, ws
+    torch.cuda.empty_cache()
+    return out
 
 
 # ---------------------------------------------------------------------------
@@ -384,6 +489,10 @@ def main() -> int:
         log(f"C5 KV write (1024-token chunk): {kw['kernel_ms'] * 1e3:.1f} us, "
             f"{kw['kernel_gbs']:.0f} GB/s, torch fk[slots]=k: {kw['ref_ms'] * 1e3:.1f} us, "
             f"exact={kw['bit_exact']}")
+        st = c5_step_leg(max(10, args.steps // 5), 10)
+        secondary["C5_step"] = st
+        log("C5 step: " + f"{st['us_per_step']:.1f} us = " + ", ".join(
+            f"{k} {v['us']:.1f} us" for k, v in st["parts"].items()))
 
     line = {
         "metric": METRIC,

@@ -223,7 +223,7 @@ static int prefill_common(const float* q, const int32_t* cu_q, int S, int max_ro
                           const void* k_cache, const void* v_cache, int kv_dtype, int num_blocks,
                           const int32_t* block_tables, const int32_t* context_lens, float* out,
                           int B, int H, int Hkv, int D, int BS, int MB, float scale,
-                          int use_mfma, void* stream) {
+                          int use_mfma, void* workspace, size_t workspace_bytes, void* stream) {
   int rc = check_attn_common(q, k_cache, v_cache, kv_dtype, num_blocks, block_tables,
                              context_lens, out, B, H, Hkv, D, BS, MB);
   if (rc != HS_OK) return rc;
@@ -240,7 +240,8 @@ static int prefill_common(const float* q, const int32_t* cu_q, int S, int max_ro
     // S is the rows of every sequence (padded form) or the longest sequence's
     // rows (ragged form): the MFMA grid is sized per sequence.
     return launch_prefill_mfma(q, cu_q, S, S, k_cache, v_cache, kv_dtype, num_blocks,
-                               block_tables, context_lens, out, B, H, Hkv, D, BS, MB, scale, st);
+                               block_tables, context_lens, out, B, H, Hkv, D, BS, MB, scale,
+                               workspace, workspace_bytes, st);
   }
   if (!valid_row_head_dim(D))
     return fail(HS_EUNSUPPORTED, "unsupported head_dim " + std::to_string(D));
@@ -270,18 +271,18 @@ static int prefill_common(const float* q, const int32_t* cu_q, int S, int max_ro
 int hs_prefill(const float* q, const void* k_cache, const void* v_cache, int kv_dtype,
                int num_blocks, const int32_t* block_tables, const int32_t* context_lens,
                float* out, int B, int S, int H, int Hkv, int D, int BS, int MB, float scale,
-               int use_mfma, void* stream) {
+               int use_mfma, void* workspace, size_t workspace_bytes, void* stream) {
   if ((int64_t)B * S > 0x7fffffffLL) return fail(HS_EINVAL, "B * S too large");
   return prefill_common(q, nullptr, S, B * S, k_cache, v_cache, kv_dtype, num_blocks,
                         block_tables, context_lens, out, B, H, Hkv, D, BS, MB, scale, use_mfma,
-                        stream);
+                        workspace, workspace_bytes, stream);
 }
 
 int hs_prefill_varlen(const float* q, const int32_t* cu_seqlens_q, int max_seqlen_q,
                       const void* k_cache, const void* v_cache, int kv_dtype, int num_blocks,
                       const int32_t* block_tables, const int32_t* context_lens, float* out,
                       int B, int H, int Hkv, int D, int BS, int MB, float scale, int use_mfma,
-                      void* stream) {
+                      void* workspace, size_t workspace_bytes, void* stream) {
   if (!cu_seqlens_q) return fail(HS_EINVAL, "null cu_seqlens_q");
   // Total rows are needed for the row grid; they are the last prefix sum,
   // which lives on the device.  The caller passes max_seqlen_q, so the grid is
@@ -289,7 +290,17 @@ int hs_prefill_varlen(const float* q, const int32_t* cu_seqlens_q, int max_seqle
   if ((int64_t)B * max_seqlen_q > 0x7fffffffLL) return fail(HS_EINVAL, "B * max_seqlen_q too large");
   return prefill_common(q, cu_seqlens_q, max_seqlen_q, B * max_seqlen_q, k_cache, v_cache,
                         kv_dtype, num_blocks, block_tables, context_lens, out, B, H, Hkv, D, BS,
-                        MB, scale, use_mfma, stream);
+                        MB, scale, use_mfma, workspace, workspace_bytes, stream);
+}
+
+size_t hs_prefill_workspace_bytes(int B, int max_seqlen_q, int H, int D, int use_mfma) {
+  if (!use_mfma || B <= 0 || max_seqlen_q <= 0 || H <= 0 || D <= 0) return 0;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  const int cus = device_cu_count(dev);
+  if (cus <= 0) return 0;
+  const PrefillPlan plan = plan_prefill_mfma(B, max_seqlen_q, H, D, cus, true);
+  return prefill_workspace_bytes(plan, B, max_seqlen_q, H, D);
 }
 
 int hs_kv_pack(const void* pool, int L, int NB, int64_t page_bytes, const int64_t* block_ids,

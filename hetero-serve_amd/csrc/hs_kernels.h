@@ -111,6 +111,16 @@ int launch_kv_append(void* k_cache, void* v_cache, int kv_dtype, int NB, int BS,
 int launch_prefill_mfma(const float* q, const int32_t* cu_q, int S, int max_rows_per_seq,
                         const void* k, const void* v, int kv_dtype, int NB, const int32_t* bt,
                         const int32_t* ctx, float* out, int B, int H, int Hkv, int D, int BS,
-                        int MB, float scale, hipStream_t stream);
+                        int MB, float scale, void* workspace, size_t workspace_bytes,
+                        hipStream_t stream);
+
+// Launch shape of the MFMA prefill (workgroup width, key-range parts) and the
+// workspace a split needs (0 without one).
+struct PrefillPlan {
+  bool wide;     // 256-row workgroups (head dim 64 and 128)
+  int n_split;   // key-range parts per query tile (1: none)
+};
+PrefillPlan plan_prefill_mfma(int B, int max_rows, int H, int D, int cus, bool can_split);
+size_t prefill_workspace_bytes(const PrefillPlan& p, int B, int max_rows, int H, int D);
 
 }  // namespace hs

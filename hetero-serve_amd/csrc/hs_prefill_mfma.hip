@@ -49,6 +49,7 @@
 #include "hs_kernels.h"
 #include "hs_mfma.h"
 
+#include <algorithm>
 #include <type_traits>
 
 namespace hs {
@@ -64,16 +65,21 @@ constexpr int kKPad = 8;                     // halves of padding per LDS K row
 constexpr int kVPad = 8;                     // halves of padding per LDS V^T row
 constexpr float kRescaleSlack = 8.0f;        // log2 units
 constexpr int kMaxRanked = 256;              // sequences a workgroup ranks itself
+constexpr int kMaxSplit = 4;                 // key-range parts of one query tile
 
-// Workgroup shape per head dim.  D 128 and 64: 8 waves (256 query rows), one
-// workgroup per CU; each K/V tile then serves twice the rows of a 4-wave
-// workgroup, which measured 3-10% faster on every prefill shape tried.  D 32
-// has too few 16-byte chunks per tile for 512 threads and keeps 4 waves.
-template <int D>
+// Workgroup shape: W waves of 32 query rows.  D 128 and 64 run 8 waves (256
+// rows, one workgroup per CU; each K/V tile then serves twice the rows of a
+// 4-wave workgroup, which measured 3-10% faster on every prefill shape tried)
+// unless the grid would leave CUs idle: then 4 waves (128 rows, two
+// workgroups per CU).  D 32 has too few 16-byte chunks per tile for 512
+// threads and always runs 4 waves.  Four waves move the K/V tiles: the first
+// half of 8, all of 4 (2 of 4 at D 32).
+template <int D, int W>
 struct Shape {
-  static constexpr int kWaves = D >= 64 ? 8 : 4;
+  static constexpr int kWaves = W;
   static constexpr int kThreads = kWaves * 64;
   static constexpr int kBM = kWaves * kRowsPerWave;   // query rows per workgroup
+  static constexpr int kProdWaves = D >= 64 ? 4 : W / 2;
 };
 
 struct PrefillArgs {
@@ -89,6 +95,13 @@ struct PrefillArgs {
   int slots_per_xcd;     // grid = kXcds * slots_per_xcd
   int ranked;            // 1: query tiles are dispatched longest first (B * n_qt <= kMaxRanked)
   float qscale;          // scale * log2(e)
+  // Key-range split (ranked dispatch only): each query tile's key tiles are
+  // cut into n_split equal parts run by separate workgroups, which write
+  // unnormalised O and (running max, sum) for prefill_merge_kernel.
+  int n_split;           // 1: no split, each workgroup writes out itself
+  int rows_cap;          // query rows per sequence in the partial arrays
+  float* part_o;         // [n_split, B, rows_cap, H, D]
+  float2* part_ml;       // [n_split, B, rows_cap, H]
 };
 
 template <int D>
@@ -113,10 +126,10 @@ struct PrefillTileLds {
 //      kG*2-byte write and 64/kG neighbouring lanes fill one V^T row segment.
 //      Its kG keys lie in one page: one block id and one base per tile.
 // The block ids of a tile are fetched by one vector load, a tile ahead.
-template <int D>
+template <int D, int W>
 struct Producer {
   static constexpr int kDC = D / 8;                         // 16-byte chunks per head row
-  static constexpr int kThreads = Shape<D>::kThreads / 2;   // the producing waves
+  static constexpr int kThreads = Shape<D, W>::kProdWaves * 64;   // the producing waves
   static constexpr int kKChunks = kBN * D / 8 / kThreads;   // K chunks per thread
   static constexpr int kG = kKChunks;                       // V keys per thread
   static constexpr int kGroups = kBN / kG;                  // V key groups per dim chunk
@@ -157,8 +170,8 @@ struct Producer {
   // in slot t % 2 and is fetched before the loads of the tile before it, so
   // waiting for it never waits for a K/V load issued later.
   template <int kSlot>
-  __device__ inline void fetch_ids(const PrefillArgs& a, const int32_t* bt, int kt) {
-    vid[kSlot] = bt[min(kt * kPages + vpage, a.MB - 1)];
+  __device__ inline void fetch_ids(const int32_t* bt, int mb, int kt) {
+    vid[kSlot] = bt[min(kt * kPages + vpage, mb - 1)];
   }
 
   template <typename T, int kSlot>
@@ -263,12 +276,13 @@ __device__ inline int seq_rows(const PrefillArgs& a, int b) {
 }
 
 template <int kBM>
-__device__ inline bool ranked_tile(const PrefillArgs& a, RankScratch& rs, int& b, int& h, int& qt) {
+__device__ inline bool ranked_tile(const PrefillArgs& a, RankScratch& rs, int& b, int& h, int& qt,
+                                   int& part) {
   const int xcd = blockIdx.x % kXcds;
   const int slot = blockIdx.x / kXcds;
   const int nh = a.H > xcd ? (a.H - xcd + kXcds - 1) / kXcds : 0;   // heads on this XCD
   if (nh == 0) return false;
-  const int r = slot / nh;
+  const int r = slot / (nh * a.n_split);   // slot = (r * n_split + part) * nh + head
   const int tid = threadIdx.x;
   if (tid < a.B) {
     const int rows = seq_rows(a, tid);
@@ -301,23 +315,25 @@ __device__ inline bool ranked_tile(const PrefillArgs& a, RankScratch& rs, int& b
   if (b < 0) return false;
   qt = rs.qt;
   h = xcd + kXcds * (slot % nh);
+  part = (slot / nh) % a.n_split;
   return true;
 }
 
-template <typename T, int D>
-__global__ __launch_bounds__(Shape<D>::kThreads) __attribute__((amdgpu_waves_per_eu(2)))
+template <typename T, int D, int W>
+__global__ __launch_bounds__((Shape<D, W>::kThreads)) __attribute__((amdgpu_waves_per_eu(2)))
 void prefill_mfma_kernel(PrefillArgs a) {
-  constexpr int kBM = Shape<D>::kBM;
+  using Sh = Shape<D, W>;
+  constexpr int kBM = Sh::kBM;
   constexpr int kDC16 = D / 16;   // 16-dim chunks (QK MFMA k-steps)
   constexpr int kDB = D / 32;     // 32-dim output blocks
   constexpr int kNKB = kBN / 32;  // 32-key blocks per tile
   __shared__ PrefillTileLds<D> lds[2];
 
   // ---- which (sequence, head, query tile) -------------------------------
-  int b, h, qt, row0, S_b, ctx_b;
+  int b, h, qt, row0, S_b, ctx_b, part = 0;
   if (a.ranked) {
     __shared__ RankScratch rank_scratch;
-    if (!ranked_tile<kBM>(a, rank_scratch, b, h, qt)) return;
+    if (!ranked_tile<kBM>(a, rank_scratch, b, h, qt, part)) return;
     row0 = rank_scratch.row0[b];
     S_b = rank_scratch.rows[b];
     ctx_b = rank_scratch.ctx[b];
@@ -348,7 +364,6 @@ void prefill_mfma_kernel(PrefillArgs a) {
   const int kvh = h / (a.H / a.Hkv);
   const int cap = a.MB * 16;        // keys the block table can address
   const int base_pos = ctx_b - S_b;     // position of row 0 of the chunk
-  const int32_t* bt = a.bt + (int64_t)b * a.MB;
 
   // This lane's query row and its inclusive key limit (-1: padding row).
   const int w_first = qt * kBM + wave * kRowsPerWave;
@@ -357,6 +372,13 @@ void prefill_mfma_kernel(PrefillArgs a) {
   const int lim = row_ok ? min(base_pos + i_row, cap - 1) : -1;
   const int last_row = min(qt * kBM + kBM, S_b) - 1;
   const int kend = min(cap, base_pos + last_row + 1);           // keys the workgroup needs
+  // This workgroup's key tiles [kt0, kt1): all of them, or its part of a split.
+  const int kt_all = kend > 0 ? (kend + kBN - 1) / kBN : 0;
+  const int kt0 = kt_all * part / a.n_split;
+  const int kt1 = kt_all * (part + 1) / a.n_split;
+  // block table from tile kt0 on (kt0 * 4 < MB, since kt_all * 64 < MB * 16 + 64)
+  const int32_t* bt = a.bt + (int64_t)b * a.MB + kt0 * (kBN / 16);
+  const int mb = a.MB - kt0 * (kBN / 16);
   const int w_lim_min = min(base_pos + w_first, cap - 1);       // first row of the wave
   const int w_lim_max = w_first < S_b ? min(base_pos + min(w_first + kRowsPerWave, S_b) - 1,
                                             cap - 1)
@@ -385,8 +407,8 @@ void prefill_mfma_kernel(PrefillArgs a) {
   // barrier per tile.
   auto run = [&](auto prod_tag) {
     constexpr bool kProd = decltype(prod_tag)::value;
-    using P = Producer<D>;
-    const int n_kt = kend > 0 ? (kend + kBN - 1) / kBN : 0;
+    using P = Producer<D, W>;
+    const int n_kt = kt1 - kt0;
     P pr;
     pr.init(a, wave, kvh);
     typename P::Regs rg;
@@ -402,8 +424,8 @@ void prefill_mfma_kernel(PrefillArgs a) {
     // the end reads a valid page, and a padding row reads the chunk's last row
     // (scaled to zero).
     if constexpr (kProd) {
-      pr.template fetch_ids<0>(a, bt, 0);
-      pr.template fetch_ids<1>(a, bt, 1);
+      pr.template fetch_ids<0>(bt, mb, 0);
+      pr.template fetch_ids<1>(bt, mb, 1);
     }
     {
       float4 x[2 * kDC16];
@@ -425,7 +447,7 @@ void prefill_mfma_kernel(PrefillArgs a) {
     }
     if constexpr (kProd) {
       pr.template store_tile<T>(lds[0], rg);
-      pr.template fetch_ids<0>(a, bt, 2);
+      pr.template fetch_ids<0>(bt, mb, 2);
       pr.template load_tile<T, 1>(a, rg);
     }
     __syncthreads();
@@ -441,16 +463,21 @@ void prefill_mfma_kernel(PrefillArgs a) {
       PrefillTileLds<D>& nxt = lds[kSet];
       const PrefillTileLds<D>& t = lds[kSet ^ 1];
       const bool fill = kt + 1 < n_kt;        // tile kt+1 sits in set kSet
-      const int tile_key0 = kt * kBN;
-      // 32-key blocks of this tile that reach this wave's rows (wave-uniform)
-      const int nkb = w_lim_max < tile_key0 ? 0 : min(kNKB, (w_lim_max - tile_key0) / 32 + 1);
+      const int tile_key0 = (kt0 + kt) * kBN;
+      // 32-key blocks of this tile that reach this wave's rows (wave-uniform);
+      // none in the padding step after an odd tile count, whose keys may still
+      // reach the rows when the range is one part of a split
+      const bool live = kMain || kt < n_kt;
+      const int nkb = !live || w_lim_max < tile_key0
+                          ? 0
+                          : min(kNKB, (w_lim_max - tile_key0) / 32 + 1);
 
   #pragma unroll
       for (int kb = 0; kb < kNKB; ++kb) {
         // Producer share of this block: V at block 0, K chunks spread over the
         // blocks; each store frees registers for the matching load of tile kt+2.
         if (kProd && kb == 0) {
-          if (kMain || kt + 3 < n_kt) pr.template fetch_ids<kSet>(a, bt, kt + 3);
+          if (kMain || kt + 3 < n_kt) pr.template fetch_ids<kSet>(bt, mb, kt + 3);
           if (fill) pr.template store_v<T>(nxt, r);
           if (load) pr.template load_v<T, kSet ^ 1>(a, r);      // tile kt+2
         }
@@ -540,15 +567,27 @@ void prefill_mfma_kernel(PrefillArgs a) {
       tile_step(S0{}, Tail{}, kt + 1);
     }
   };
-  if (wave < Shape<D>::kWaves / 2) run(std::true_type{});
+  if (wave < Sh::kProdWaves) run(std::true_type{});
   else run(std::false_type{});
 
   // ---- normalise and store: lane (j, hh) owns query j and dims
   // d*32 + 8*g + 4*hh + (0..3) ----
   const float lsum = sum_halves(l);
   if (!row_ok) return;
-  const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
-  float* op = a.out + ((int64_t)(row0 + i_row) * a.H + h) * D + 4 * hh;
+  float inv;
+  float* op;
+  if (a.n_split > 1) {
+    // one part of a split: unnormalised O and (running max, sum) for the merge
+    // (rows past rows_cap, which a too-small max_seqlen_q leaves, have no slot)
+    if (i_row >= a.rows_cap) return;
+    const int64_t pair = ((int64_t)(part * a.B + b) * a.rows_cap + i_row) * a.H + h;
+    if (hh == 0) a.part_ml[pair] = make_float2(m, lsum);
+    inv = 1.0f;
+    op = a.part_o + pair * D + 4 * hh;
+  } else {
+    inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
+    op = a.out + ((int64_t)(row0 + i_row) * a.H + h) * D + 4 * hh;
+  }
 #pragma unroll
   for (int d = 0; d < kDB; ++d)
 #pragma unroll
@@ -558,29 +597,88 @@ void prefill_mfma_kernel(PrefillArgs a) {
                       o[d][4 * g + 3] * inv);
 }
 
-// Grid plan for one head dim: query tiles of Shape<D>::kBM rows, longest
-// first when the batch has at most kMaxRanked sequences.
-template <typename T, int D>
+// Merge of a split prefill: for row i of sequence b and head h,
+//   out = sum_p w_p O_p / sum_p w_p l_p,  w_p = exp2(m_p - max_p m_p)
+// over the n_split parts (a part without keys for the row has m_p = -3e38 and
+// weight 0; a row without keys gets zeros, as in the unsplit kernel).  One
+// thread per 4 dims; the partial arrays are read once, out written once.
+template <int D>
+__global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a) {
+  constexpr int kC = D / 4;
+  const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t n_pairs = (int64_t)a.B * a.rows_cap * a.H;   // pairs per part
+  const int64_t pair = g / kC;
+  if (pair >= n_pairs) return;
+  const int c = (int)(g - pair * kC);
+  const int h = (int)(pair % a.H);
+  const int64_t bi = pair / a.H;
+  const int i = (int)(bi % a.rows_cap);
+  const int b = (int)(bi / a.rows_cap);
+  if (i >= seq_rows(a, b)) return;
+  const int64_t row0 = a.cu_q ? a.cu_q[b] : (int64_t)b * a.S;
+  float2 ml[kMaxSplit];
+  float mx = kNegBig;
+#pragma unroll
+  for (int p = 0; p < kMaxSplit; ++p) {
+    if (p < a.n_split) {
+      ml[p] = a.part_ml[p * n_pairs + pair];
+      mx = fmaxf(mx, ml[p].x);
+    }
+  }
+  float lsum = 0.0f;
+  float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+  for (int p = 0; p < kMaxSplit; ++p) {
+    if (p < a.n_split) {
+      const float w = fast_exp2(ml[p].x - mx);
+      const float4 o = reinterpret_cast<const float4*>(a.part_o)[(p * n_pairs + pair) * kC + c];
+      lsum += w * ml[p].y;
+      acc.x += w * o.x;
+      acc.y += w * o.y;
+      acc.z += w * o.z;
+      acc.w += w * o.w;
+    }
+  }
+  const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
+  reinterpret_cast<float4*>(a.out)[((row0 + i) * a.H + h) * kC + c] =
+      make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
+}
+
+// Grid plan for one head dim and width: query tiles of W * 32 rows, longest
+// first when the batch has at most kMaxRanked sequences; a split multiplies
+// each ranked tile's slots by n_split (parts next to each other).
+template <typename T, int D, int W>
 int launch_typed(PrefillArgs a, int max_rows_per_seq, hipStream_t stream) {
-  constexpr int kBM = Shape<D>::kBM;
+  constexpr int kBM = Shape<D, W>::kBM;
   a.n_qt = (max_rows_per_seq + kBM - 1) / kBM;
   const int64_t pairs = (int64_t)a.B * a.H;
   a.ranked = a.B <= kMaxRanked;
-  const int64_t slots = a.ranked ? (int64_t)a.B * a.n_qt * ((a.H + kXcds - 1) / kXcds)
-                                 : (pairs + kXcds - 1) / kXcds * a.n_qt;
+  if (a.n_split > 1 && !a.ranked) return fail(HS_EUNSUPPORTED, "split prefill needs ranked tiles");
+  const int64_t slots =
+      a.ranked ? (int64_t)a.B * a.n_qt * ((a.H + kXcds - 1) / kXcds) * a.n_split
+               : (pairs + kXcds - 1) / kXcds * a.n_qt;
   if (slots * kXcds > 0x7fffffffLL) return fail(HS_EUNSUPPORTED, "prefill grid too large");
   a.slots_per_xcd = (int)slots;
-  const dim3 grid((unsigned)(kXcds * a.slots_per_xcd)), block(Shape<D>::kThreads);
-  hipLaunchKernelGGL((prefill_mfma_kernel<T, D>), grid, block, 0, stream, a);
+  const dim3 grid((unsigned)(kXcds * a.slots_per_xcd)), block(Shape<D, W>::kThreads);
+  hipLaunchKernelGGL((prefill_mfma_kernel<T, D, W>), grid, block, 0, stream, a);
+  if (a.n_split > 1) {
+    const int64_t threads = (int64_t)a.B * a.rows_cap * a.H * (D / 4);
+    hipLaunchKernelGGL((prefill_merge_kernel<D>), dim3((unsigned)((threads + 255) / 256)),
+                       dim3(256), 0, stream, a);
+  }
   return HS_OK;
 }
 
 template <typename T>
-int launch_dim(const PrefillArgs& a, int D, int max_rows_per_seq, hipStream_t stream) {
+int launch_dim(const PrefillArgs& a, int D, bool wide, int max_rows_per_seq, hipStream_t stream) {
   switch (D) {
-    case 32: return launch_typed<T, 32>(a, max_rows_per_seq, stream);
-    case 64: return launch_typed<T, 64>(a, max_rows_per_seq, stream);
-    case 128: return launch_typed<T, 128>(a, max_rows_per_seq, stream);
+    case 32: return launch_typed<T, 32, 4>(a, max_rows_per_seq, stream);
+    case 64:
+      return wide ? launch_typed<T, 64, 8>(a, max_rows_per_seq, stream)
+                  : launch_typed<T, 64, 4>(a, max_rows_per_seq, stream);
+    case 128:
+      return wide ? launch_typed<T, 128, 8>(a, max_rows_per_seq, stream)
+                  : launch_typed<T, 128, 4>(a, max_rows_per_seq, stream);
     default: return fail(HS_EUNSUPPORTED, "unsupported head_dim for the MFMA path: " +
                                               std::to_string(D));
   }
@@ -588,10 +686,35 @@ int launch_dim(const PrefillArgs& a, int D, int max_rows_per_seq, hipStream_t st
 
 }  // namespace
 
+// Launch shape of the MFMA prefill for B sequences of up to max_rows query
+// rows on a device with `cus` CUs.  Full-width workgroups (256 rows; 128 at
+// head dim 32) when their query tiles cover every CU.  Otherwise, with a
+// workspace, each tile's key range is split over floor(cus / tiles) <= 4
+// workgroups (a 1024-row chunk of 32 heads: 128 tiles, 2 parts); without one,
+// 128-row workgroups, which run one wave per SIMD but reach twice as many CUs.
+PrefillPlan plan_prefill_mfma(int B, int max_rows, int H, int D, int cus, bool can_split) {
+  const int bm = D >= 64 ? 256 : 128;
+  const int64_t tiles = (int64_t)B * ((max_rows + bm - 1) / bm) * H;
+  PrefillPlan p{true, 1};
+  if (tiles >= cus) return p;
+  const int64_t splits = std::min<int64_t>(kMaxSplit, tiles > 0 ? cus / tiles : 1);
+  if (can_split && splits >= 2 && B <= kMaxRanked) p.n_split = (int)splits;
+  else p.wide = false;
+  return p;
+}
+
+size_t prefill_workspace_bytes(const PrefillPlan& p, int B, int max_rows, int H, int D) {
+  if (p.n_split < 2) return 0;
+  const size_t pairs = (size_t)p.n_split * B * max_rows * H;
+  const size_t o_bytes = (pairs * D * sizeof(float) + 255) / 256 * 256;
+  return o_bytes + pairs * sizeof(float2);
+}
+
 int launch_prefill_mfma(const float* q, const int32_t* cu_q, int S, int max_rows_per_seq,
                         const void* k, const void* v, int kv_dtype, int NB, const int32_t* bt,
                         const int32_t* ctx, float* out, int B, int H, int Hkv, int D, int BS,
-                        int MB, float scale, hipStream_t stream) {
+                        int MB, float scale, void* workspace, size_t workspace_bytes,
+                        hipStream_t stream) {
   (void)BS;  // validated to be 16 by the caller
   PrefillArgs a{};
   a.q = q;
@@ -608,10 +731,26 @@ int launch_prefill_mfma(const float* q, const int32_t* cu_q, int S, int max_rows
   a.MB = MB;
   a.NB = NB;
   a.qscale = scale * kLog2e;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return fail(HS_EHIP, "hipGetDevice failed");
+  const int cus = hs_device_cu_count(dev);
+  if (cus <= 0) return fail(HS_EHIP, "could not read the device CU count");
+  const PrefillPlan plan = plan_prefill_mfma(B, max_rows_per_seq, H, D, cus, workspace != nullptr);
+  a.n_split = plan.n_split;
+  a.rows_cap = max_rows_per_seq;
+  if (plan.n_split > 1) {
+    const size_t need = prefill_workspace_bytes(plan, B, max_rows_per_seq, H, D);
+    if (workspace_bytes < need)
+      return fail(HS_EWORKSPACE, "prefill workspace too small: " + std::to_string(need) +
+                                     " bytes needed");
+    const size_t o_bytes = need - (size_t)plan.n_split * B * max_rows_per_seq * H * sizeof(float2);
+    a.part_o = static_cast<float*>(workspace);
+    a.part_ml = reinterpret_cast<float2*>(static_cast<char*>(workspace) + o_bytes);
+  }
   profile_begin(stream);
   int rc;
-  if (kv_dtype == HS_DTYPE_F16) rc = launch_dim<_Float16>(a, D, max_rows_per_seq, stream);
-  else rc = launch_dim<Bf16>(a, D, max_rows_per_seq, stream);
+  if (kv_dtype == HS_DTYPE_F16) rc = launch_dim<_Float16>(a, D, plan.wide, max_rows_per_seq, stream);
+  else rc = launch_dim<Bf16>(a, D, plan.wide, max_rows_per_seq, stream);
   profile_end(stream);
   if (rc != HS_OK) return rc;
   return check_launch("MFMA prefill");

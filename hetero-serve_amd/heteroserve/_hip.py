@@ -22,7 +22,7 @@ import threading
 from pathlib import Path
 from typing import Optional
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
 
 _lock = threading.Lock()
@@ -44,12 +44,13 @@ _SIGNATURES = {
     "hs_decode": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_vp, _c_vp, _c_vp,
                            _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float,
                            _c_int, _c_int, _c_vp, _c_size, _c_vp]),
+    "hs_prefill_workspace_bytes": (_c_size, [_c_int] * 5),
     "hs_prefill": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_vp, _c_vp, _c_vp,
                             _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
-                            _c_float, _c_int, _c_vp]),
+                            _c_float, _c_int, _c_vp, _c_size, _c_vp]),
     "hs_prefill_varlen": (_c_int, [_c_vp, _c_vp, _c_int, _c_vp, _c_vp, _c_int, _c_int,
                                    _c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_int,
-                                   _c_int, _c_int, _c_float, _c_int, _c_vp]),
+                                   _c_int, _c_int, _c_float, _c_int, _c_vp, _c_size, _c_vp]),
     "hs_kv_pack": (_c_int, [_c_vp, _c_int, _c_int, _c_i64, _c_vp, _c_int, _c_vp, _c_vp]),
     "hs_kv_unpack": (_c_int, [_c_vp, _c_int, _c_int, _c_i64, _c_vp, _c_int, _c_vp, _c_vp]),
     "hs_kv_gather": (_c_int, [_c_vp, _c_int, _c_int, _c_i64, _c_vp, _c_int, _c_int, _c_int,
@@ -253,8 +254,23 @@ def decode(q, k_cache, v_cache, block_tables, context_lens, scale: float,
     return out
 
 
-def prefill(q, k_cache, v_cache, block_tables, context_lens, scale: float, use_mfma: bool):
-    """out[B, S, H, D] fp32 = causal chunked prefill via hs_prefill."""
+def _prefill_workspace(L, B: int, rows: int, H: int, D: int, use_mfma: bool, split: bool,
+                       device):
+    """(tensor or None, bytes): the key-range split's scratch, when it applies."""
+    import torch
+
+    nbytes = L.hs_prefill_workspace_bytes(B, rows, H, D, int(bool(use_mfma))) if split else 0
+    if not nbytes:
+        return None, 0
+    return torch.empty(nbytes, dtype=torch.uint8, device=device), nbytes
+
+
+def prefill(q, k_cache, v_cache, block_tables, context_lens, scale: float, use_mfma: bool,
+            split: bool = True):
+    """out[B, S, H, D] fp32 = causal chunked prefill via hs_prefill.
+
+    split=False passes no workspace, so the matrix-core kernel runs without
+    the key-range split (for tests of that launch shape)."""
     import torch
 
     L = lib()
@@ -275,16 +291,19 @@ def prefill(q, k_cache, v_cache, block_tables, context_lens, scale: float, use_m
     if B == 0 or S == 0:
         return out
     with _DeviceGuard(q.device):
+        ws, ws_bytes = _prefill_workspace(L, B, S, H, D, use_mfma, split, q.device)
         check(L.hs_prefill(
             q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), dtype_code(k_cache.dtype),
             NB, bt.data_ptr(), ctx.data_ptr(), out.data_ptr(), B, S, H, Hkv, D, BS,
-            bt.shape[1], float(scale), int(bool(use_mfma)), stream_of(q.device)))
+            bt.shape[1], float(scale), int(bool(use_mfma)),
+            ws.data_ptr() if ws is not None else None, ws_bytes, stream_of(q.device)))
     return out
 
 
 def prefill_varlen(q, cu_seqlens_q, max_seqlen_q: int, k_cache, v_cache, block_tables,
-                   context_lens, scale: float, use_mfma: bool):
-    """out[T, H, D] fp32 for ragged chunks via hs_prefill_varlen."""
+                   context_lens, scale: float, use_mfma: bool, split: bool = True):
+    """out[T, H, D] fp32 for ragged chunks via hs_prefill_varlen (split as for
+    prefill)."""
     import torch
 
     L = lib()
@@ -305,11 +324,14 @@ def prefill_varlen(q, cu_seqlens_q, max_seqlen_q: int, k_cache, v_cache, block_t
     if B == 0 or T == 0:
         return out
     with _DeviceGuard(q.device):
+        ws, ws_bytes = _prefill_workspace(L, B, int(max_seqlen_q), H, D, use_mfma, split,
+                                          q.device)
         check(L.hs_prefill_varlen(
             q.data_ptr(), cu.data_ptr(), int(max_seqlen_q), k_cache.data_ptr(),
             v_cache.data_ptr(), dtype_code(k_cache.dtype), NB, bt.data_ptr(), ctx.data_ptr(),
             out.data_ptr(), B, H, Hkv, D, BS, bt.shape[1], float(scale),
-            int(bool(use_mfma)), stream_of(q.device)))
+            int(bool(use_mfma)), ws.data_ptr() if ws is not None else None, ws_bytes,
+            stream_of(q.device)))
     return out
 
 

@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define HS_ABI_VERSION 2
+#define HS_ABI_VERSION 3
 
 /* KV element type codes (the pool dtype). */
 #define HS_DTYPE_F32 0
@@ -123,6 +123,18 @@ int hs_decode(const float* q, const void* k_cache, const void* v_cache, int kv_d
               size_t workspace_bytes, void* stream);
 
 /*
+ * Workspace bytes hs_prefill / hs_prefill_varlen may use for B sequences of
+ * up to max_seqlen_q query rows (S for hs_prefill), for the current HIP
+ * device; 0 when they need none.  Only the matrix-core path (use_mfma = 1)
+ * uses one: when its query tiles cannot cover every CU, each tile's key range
+ * is split over up to 4 workgroups, whose partial results (fp32, (D + 2) * 4
+ * bytes per part, row and head) are merged by a second kernel.  No reference
+ * counterpart (the reference's prefill has no split); version 3 of the ABI
+ * added it and the workspace arguments below.
+ */
+size_t hs_prefill_workspace_bytes(int B, int max_seqlen_q, int H, int D, int use_mfma);
+
+/*
  * Causal chunked prefill over the paged cache.  Query s of sequence b sits at
  * absolute position ctx_b - S + s and attends to keys [0, ctx_b - S + s]; rows
  * whose position is negative (padding in front of a short sequence) are zero.
@@ -138,11 +150,16 @@ int hs_decode(const float* q, const void* k_cache, const void* v_cache, int kv_d
  *                 f16 or bf16, BS == 16, D in {32,64,128})
  *
  *   q   [B, S, H, D] float32;  out [B, S, H, D] float32
+ *   workspace  NULL, or device scratch of hs_prefill_workspace_bytes(B, S, H,
+ *              D, use_mfma) bytes.  NULL runs without the key-range split
+ *              (narrower workgroups instead); a workspace smaller than the
+ *              split needs is HS_EWORKSPACE.  Calls that overlap in time must
+ *              not share one.
  */
 int hs_prefill(const float* q, const void* k_cache, const void* v_cache, int kv_dtype,
                int num_blocks, const int32_t* block_tables, const int32_t* context_lens,
                float* out, int B, int S, int H, int Hkv, int D, int BS, int MB, float scale,
-               int use_mfma, void* stream);
+               int use_mfma, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Ragged-batch form of hs_prefill (use_mfma as there): sequence b owns query
@@ -151,13 +168,14 @@ int hs_prefill(const float* q, const void* k_cache, const void* v_cache, int kv_
  * sequence b sits at position ctx_b - S_b + i.  No reference counterpart: the
  * reference's engine calls prefill with B = 1 per chunk
  * (heteroserve/model/torch_engine.py:292-313), and this entry point runs
- * several such chunks in one launch.
+ * several such chunks in one launch.  workspace as for hs_prefill, sized by
+ * hs_prefill_workspace_bytes(B, max_seqlen_q, H, D, use_mfma).
  */
 int hs_prefill_varlen(const float* q, const int32_t* cu_seqlens_q, int max_seqlen_q,
                       const void* k_cache, const void* v_cache, int kv_dtype, int num_blocks,
                       const int32_t* block_tables, const int32_t* context_lens, float* out,
                       int B, int H, int Hkv, int D, int BS, int MB, float scale,
-                      int use_mfma, void* stream);
+                      int use_mfma, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * KV-block pack for migration:

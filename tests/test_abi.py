@@ -40,7 +40,7 @@ def test_header_declarations_are_bound_by_the_loader():
 def test_library_exports_every_declared_symbol(lib):
     for name in _declared_functions():
         assert hasattr(lib, name), name
-    assert lib.hs_abi_version() == 2
+    assert lib.hs_abi_version() == 3
     assert lib.hs_last_error() == b""
 
 
@@ -68,11 +68,13 @@ def test_argument_errors_need_no_device(lib):
     assert rc == -4 and b"workspace" in lib.hs_last_error()
     assert lib.hs_decode_workspace_bytes(2, 4, 4, 64, 16, 64, 1, 0) == 0      # one pass
     assert lib.hs_decode_workspace_bytes(2, 4, 4, 64, 16, 64, 0, 24) == 0     # bad partition
+    assert lib.hs_prefill_workspace_bytes(1, 1024, 32, 128, 0) == 0          # row kernel
+    assert lib.hs_prefill_workspace_bytes(0, 1024, 32, 128, 1) == 0          # nothing to do
     rc = lib.hs_prefill(fake, fake, fake, 0, 8, fake, fake, fake, 1, 4, 4, 4, 64, 16, 2,
-                        0.1, 1, None)
+                        0.1, 1, None, 0, None)
     assert rc == -2 and b"fp16 or bf16" in lib.hs_last_error()
     rc = lib.hs_prefill(fake, fake, fake, 1, 8, fake, fake, fake, 1, 4, 4, 4, 64, 32, 2,
-                        0.1, 1, None)
+                        0.1, 1, None, 0, None)
     assert rc == -2 and b"block_size == 16" in lib.hs_last_error()
     rc = lib.hs_kv_pack(None, 1, 8, 1024, None, 3, None, None)
     assert rc == -1

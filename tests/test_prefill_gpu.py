@@ -237,3 +237,45 @@ def test_mfma_dispatch_orders(n_seq, H, Hkv):
         want = prefill_one(qb.cpu(), case.k_cache.cpu(), case.v_cache.cpu(),
                            case.block_tables[b].cpu(), int(case.ctx[b]), case.scale)
         assert _maxerr(got[cu[b]:cu[b + 1]], want) <= 2e-3, b
+
+
+@pytest.mark.parametrize("prefix,chunk,H,Hkv,D", [
+    ([0], [100], 4, 4, 128),                  # 2 key tiles over 4 parts: empty parts
+    ([0, 100, 700], [40, 1, 300], 8, 2, 64),  # ragged, GQA, 4 parts
+    ([64, 0], [200, 130], 4, 4, 32),          # 128-row tiles at head dim 32
+    ([1500], [700], 16, 4, 128),              # 48 tiles: 4 parts of 8-12 key tiles
+])
+def test_mfma_key_split(prefix, chunk, H, Hkv, D):
+    """Grids too small to cover the CUs split each query tile's key range
+    over up to 4 workgroups and merge their partial softmax states; without
+    a workspace the same call runs 128-row workgroups instead.  Both against
+    the per-sequence oracle, 2e-3."""
+    from heteroserve import _hip
+    from hsbench.cases import build_prefill
+
+    _wmma()
+    need = int(sum(-(-(p + s) // 16) for p, s in zip(prefix, chunk)))
+    case = build_prefill("t", np.array(prefix), np.array(chunk), H, Hkv, D, need + 8,
+                         torch.bfloat16, DEV, seed=sum(chunk) + D)
+    lib = _hip.lib()
+    assert lib.hs_prefill_workspace_bytes(len(prefix), max(chunk), H, D, 1) > 0
+    cu = case.cu_seqlens.cpu().numpy()
+    for split in (True, False):
+        got = _hip.prefill_varlen(case.q, case.cu_seqlens, max(chunk), case.k_cache,
+                                  case.v_cache, case.block_tables, case.context_lens,
+                                  case.scale, use_mfma=True, split=split)
+        for b in range(len(prefix)):
+            want = prefill_one(case.q[cu[b]:cu[b + 1]].cpu(), case.k_cache.cpu(),
+                               case.v_cache.cpu(), case.block_tables[b].cpu(),
+                               int(case.ctx[b]), case.scale)
+            err = _maxerr(got[cu[b]:cu[b + 1]], want)
+            assert err <= 2e-3, (split, b, err)
+
+
+def test_mfma_key_split_padded_rows():
+    """The padded form through the split: rows at negative positions stay 0."""
+    wm = _wmma()
+    pool, bt, ctx, q, scale = _ref_prefill([64, 10], 32, None, seed=5, dtype=torch.float16)
+    got = wm.paged_attention_prefill_wmma(q, pool[0, 0], pool[0, 1], bt, ctx, scale).cpu()
+    assert torch.all(got[1, :22] == 0)
+    assert _maxerr(got, _oracle(q, pool[0, 0], pool[0, 1], bt, ctx, scale)) <= 2e-3
