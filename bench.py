@@ -53,14 +53,21 @@ def log(*a) -> None:
 TRAFFIC_PROFILE = ROOT / "profiles" / "decode_C2_prefill_C4_pack_C5.md"
 # The headline leg's dominant kernel, as rocprofv3 names it.
 DECODE_KERNEL = "hs::row_attn_part_kernel<hs::Bf16, 128, true, 1>"
+# C2's launch of it: 64 rows x 16 partitions of 512 tokens x 16 two-head
+# workgroups.  The PMC summary lists a kernel launched with several grid sizes
+# once per size, as "<name> [<n> workgroups]".
+DECODE_WORKGROUPS = 16384
 
 
-def profiled_traffic(kernel: str):
-    """HBM read + write bytes of `kernel` from the committed PMC summary."""
+def profiled_traffic(kernel: str, workgroups: int):
+    """HBM read + write bytes of `kernel`'s launch of `workgroups` workgroups
+    from the committed PMC summary."""
+    names = (kernel, f"{kernel} [{workgroups} workgroups]")
     try:
-        for line in TRAFFIC_PROFILE.read_text().splitlines():
+        text = TRAFFIC_PROFILE.read_text()
+        for line in text[text.index("# HBM traffic per launch"):].splitlines():
             cells = [c.strip(" `") for c in line.split("|")]
-            if len(cells) == 7 and cells[1] == kernel and "." in cells[4]:
+            if len(cells) == 7 and cells[1] in names and "." in cells[4]:
                 return int(round((float(cells[4]) + float(cells[5])) * 1e9))
     except (OSError, ValueError):
         pass
@@ -517,7 +524,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(dec["kernel_gbs"] / HBM_PEAK_GBS, 4),
-            "traffic": profiled_traffic(DECODE_KERNEL)
+            "traffic": profiled_traffic(DECODE_KERNEL, DECODE_WORKGROUPS)
             if args.config == "C2" and not args.partition else None,
             "traffic_source": TRAFFIC_PROFILE.name,
             "algorithmic_bytes": dec["bytes"],

@@ -213,7 +213,11 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void row_attn_part_kernel(RowAtt
 
 // Log-sum-exp merge of the partition states of every (row, head) that has
 // more than one non-empty partition (reference: merge_splits_kernel,
-// paged_attn_v3.py:170-208).  One wave per (row, head), lanes over D.
+// paged_attn_v3.py:170-208).  One wave per (row, head), lanes over D.  The
+// kernel is latency-bound (a few MB in all), so its memory round trips are
+// batched: lane p reads partition p's (max, sum), 64 partitions per load, and
+// the partial outputs are read 8 partitions at a time, each weight taken from
+// the lane that computed it.
 template <int D>
 __global__ __launch_bounds__(256) void row_attn_merge_kernel(RowAttnArgs a) {
   const int lane = threadIdx.x & 63;
@@ -226,25 +230,46 @@ __global__ __launch_bounds__(256) void row_attn_merge_kernel(RowAttnArgs a) {
   partition_range(a, end, 0, lo, hi, nparts);
   if (nparts <= 1) return;  // written directly by the partition kernel
 
-  const float* ml = a.part_ml + w * a.P * 2;
-  float mm = kNegBig;
-  for (int p = 0; p < nparts; ++p) mm = fmaxf(mm, ml[2 * p]);
+  const float2* ml = reinterpret_cast<const float2*>(a.part_ml) + w * a.P;
+  const float2 none = make_float2(kNegBig, 0.0f);
+  const float2 st0 = lane < nparts ? ml[lane] : none;
+  float mm = st0.x;
+  for (int p0 = 64; p0 < nparts; p0 += 64)
+    if (p0 + lane < nparts) mm = fmaxf(mm, ml[p0 + lane].x);
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) mm = fmaxf(mm, __shfl_xor(mm, off));
 
   constexpr int kPer = (D + 63) / 64;
+  constexpr int kBatch = 8;
   float acc[kPer];
 #pragma unroll
   for (int i = 0; i < kPer; ++i) acc[i] = 0.0f;
-  float lsum = 0.0f;
-  for (int p = 0; p < nparts; ++p) {
-    const float wt = fast_exp2(ml[2 * p] - mm);
-    lsum = fmaf(ml[2 * p + 1], wt, lsum);
-    const float* pa = a.part_acc + (w * a.P + p) * D;
+  float lsum = 0.0f;   // this lane's partitions; summed over the wave below
+  for (int p0 = 0; p0 < nparts; p0 += 64) {
+    const int n = min(64, nparts - p0);
+    const float2 st = p0 == 0 ? st0 : (lane < n ? ml[p0 + lane] : none);
+    const float wt = lane < n ? fast_exp2(st.x - mm) : 0.0f;
+    lsum = fmaf(st.y, wt, lsum);
+    const float* pa = a.part_acc + (w * a.P + p0) * D;
+    for (int p = 0; p < n; p += kBatch) {
+      float v[kBatch][kPer];
 #pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-      const int d = lane + 64 * i;
-      if (d < D) acc[i] = fmaf(pa[d], wt, acc[i]);
+      for (int u = 0; u < kBatch; ++u)
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+          const int d = lane + 64 * i;
+          v[u][i] = (p + u < n && d < D) ? pa[(p + u) * D + d] : 0.0f;
+        }
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const float wu = __builtin_bit_cast(
+            float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wt), min(p + u, 63)));
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) acc[i] = fmaf(v[u][i], wu, acc[i]);
+      }
     }
   }
+  lsum = group_sum<64>(lsum);
   const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {

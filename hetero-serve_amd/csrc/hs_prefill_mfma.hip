@@ -15,7 +15,9 @@
 // workgroup per CU: a wave's softmax (VALU) then runs while the other wave of
 // its SIMD issues MFMAs, which measured faster than 64 rows per wave at one
 // wave per SIMD, even though each LDS fragment then feeds one MFMA instead of
-// two.
+// two.  A grid too small for the CUs (one chunk of one sequence) splits each
+// query tile's keys over up to 4 workgroups whose partial softmax states
+// prefill_merge_kernel combines.
 // Scores are computed transposed, S^T = K . Q^T, with v_mfma_f32_32x32x16_f16:
 // K rows are the A operand (read from LDS), Q^T the B operand (held in
 // registers for the whole walk).  The accumulator then has one query per
@@ -69,9 +71,10 @@ constexpr int kMaxSplit = 4;                 // key-range parts of one query til
 
 // Workgroup shape: W waves of 32 query rows.  D 128 and 64 run 8 waves (256
 // rows, one workgroup per CU; each K/V tile then serves twice the rows of a
-// 4-wave workgroup, which measured 3-10% faster on every prefill shape tried)
-// unless the grid would leave CUs idle: then 4 waves (128 rows, two
-// workgroups per CU).  D 32 has too few 16-byte chunks per tile for 512
+// 4-wave workgroup, which measured 3-10% faster on every prefill shape tried).
+// When those tiles cannot cover the CUs, the key range is split instead
+// (plan_prefill_mfma); without a workspace for that, 4 waves (128 rows) reach
+// twice as many CUs.  D 32 has too few 16-byte chunks per tile for 512
 // threads and always runs 4 waves.  Four waves move the K/V tiles: the first
 // half of 8, all of 4 (2 of 4 at D 32).
 template <int D, int W>
@@ -96,7 +99,7 @@ struct PrefillArgs {
   int ranked;            // 1: query tiles are dispatched longest first (B * n_qt <= kMaxRanked)
   float qscale;          // scale * log2(e)
   // Key-range split (ranked dispatch only): each query tile's key tiles are
-  // cut into n_split equal parts run by separate workgroups, which write
+  // cut into up to n_split parts run by separate workgroups, which write
   // unnormalised O and (running max, sum) for prefill_merge_kernel.
   int n_split;           // 1: no split, each workgroup writes out itself
   int rows_cap;          // query rows per sequence in the partial arrays
@@ -372,13 +375,22 @@ void prefill_mfma_kernel(PrefillArgs a) {
   const int lim = row_ok ? min(base_pos + i_row, cap - 1) : -1;
   const int last_row = min(qt * kBM + kBM, S_b) - 1;
   const int kend = min(cap, base_pos + last_row + 1);           // keys the workgroup needs
-  // This workgroup's key tiles [kt0, kt1): all of them, or its part of a split.
+  // This workgroup's key tiles [kt0, kt1): all of them, or its part of a
+  // split.  Every query tile of a sequence cuts at the same key tiles (parts
+  // of ceil(T / n_split) tiles, T = the sequence's last tile's count), so the
+  // workgroups of one part stream the same K/V at the same time; the longest
+  // tile's parts set the span either way.
   const int kt_all = kend > 0 ? (kend + kBN - 1) / kBN : 0;
-  const int kt0 = kt_all * part / a.n_split;
-  const int kt1 = kt_all * (part + 1) / a.n_split;
-  // block table from tile kt0 on (kt0 * 4 < MB, since kt_all * 64 < MB * 16 + 64)
-  const int32_t* bt = a.bt + (int64_t)b * a.MB + kt0 * (kBN / 16);
-  const int mb = a.MB - kt0 * (kBN / 16);
+  const int kt_seq = (min(cap, ctx_b) + kBN - 1) / kBN;
+  const int per_part = (kt_seq + a.n_split - 1) / a.n_split;
+  const int kt0 = min(kt_all, part * per_part);
+  const int kt1 = min(kt_all, kt0 + per_part);
+  // Block table from tile kt0 on.  A non-empty part has kt0 * 4 < MB (since
+  // kt_all * 64 < MB * 16 + 64); an empty one consumes no tile, and its
+  // prologue loads stay in the table through the clamp.
+  const int pg0 = min(kt0, (a.MB - 1) / (kBN / 16)) * (kBN / 16);
+  const int32_t* bt = a.bt + (int64_t)b * a.MB + pg0;
+  const int mb = a.MB - pg0;
   const int w_lim_min = min(base_pos + w_first, cap - 1);       // first row of the wave
   const int w_lim_max = w_first < S_b ? min(base_pos + min(w_first + kRowsPerWave, S_b) - 1,
                                             cap - 1)
