@@ -30,6 +30,7 @@
 namespace hs {
 
 constexpr int kDecodeWaves = 2;  // waves per workgroup
+constexpr float kDecodeSlack = 8.0f;  // lazy raise of the running max, log2 units
 
 // One wave = G query heads of one KV group for one (row, partition): each
 // 16-byte K/V load feeds G dot products, so a GQA group's pages are read once
@@ -148,18 +149,24 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void row_attn_part_kernel(RowAtt
         sc[u] = ok[u] ? d : kNegBig;
         mx = fmaxf(mx, sc[u]);
       }
-      const float m_new = fmaxf(m[g], mx);
-      const float corr = fast_exp2(m[g] - m_new);
+      // The running max is raised only when this step's max exceeds it by
+      // more than kDecodeSlack (log2 units): probabilities stay <= 2^slack in
+      // fp32 and the G accumulators are rescaled on few steps.
+      if (__builtin_amdgcn_ballot_w64(mx > m[g] + kDecodeSlack) != 0) {
+        const float m_new = fmaxf(m[g], mx);
+        const float corr = fast_exp2(m[g] - m_new);
+        l[g] *= corr;
+#pragma unroll
+        for (int e = 0; e < kVec; ++e) acc[g][e] *= corr;
+        m[g] = m_new;
+      }
       float psum = 0.0f;
 #pragma unroll
       for (int u = 0; u < kU; ++u) {
-        pu[g][u] = ok[u] ? fast_exp2(sc[u] - m_new) : 0.0f;
+        pu[g][u] = ok[u] ? fast_exp2(sc[u] - m[g]) : 0.0f;
         psum += pu[g][u];
       }
-      l[g] = fmaf(l[g], corr, psum);
-#pragma unroll
-      for (int e = 0; e < kVec; ++e) acc[g][e] *= corr;
-      m[g] = m_new;
+      l[g] += psum;
     }
 #pragma unroll
     for (int u = 0; u < kU; ++u) {
