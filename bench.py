@@ -255,8 +255,10 @@ def c5_step_leg(steps: int, warmup: int) -> dict:
     into its cache (1024 tokens at positions 2048..3071, fp32 slices of a fused
     QKV output), its causal attention on the matrix cores, the 255 decode
     tokens' K/V appended at ctx - 1, the decode of those 255 sequences (half
-    of them sharing a 1024-token prefix), and the 4096-block migration pack of
-    the decode pool.  Returns the step time and each part timed alone."""
+    of them sharing a 1024-token prefix: hs_decode_shared, which reads a
+    partition that several sequences hold once for all of them), and the
+    4096-block migration pack of the decode pool.  Returns the step time,
+    each part timed alone, and the plain hs_decode of the same batch."""
     import torch
 
     from heteroserve import _hip
@@ -284,7 +286,7 @@ def c5_step_leg(steps: int, warmup: int) -> dict:
     dpos = (dc.context_lens - 1).to(torch.int32).contiguous()
     dseq = torch.arange(B, dtype=torch.int32, device=dev)
     dout = torch.empty((B, H, D), dtype=torch.float32, device=dev)
-    ws_bytes = lib.hs_decode_workspace_bytes(B, H, hkv, D, bs, dmb, 0, 0)
+    ws_bytes = lib.hs_decode_shared_workspace_bytes(B, H, hkv, D, bs, dmb, 0)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
     ids = torch.as_tensor(cases.c5_pack_ids(dnb), dtype=torch.int64, device=dev)
     pool = dc.pool
@@ -308,10 +310,10 @@ def c5_step_leg(steps: int, warmup: int) -> dict:
             dkc.data_ptr(), dvc.data_ptr(), kdt, dnb, bs, hkv, D, dc.block_tables.data_ptr(), dmb,
             dpos.data_ptr(), dseq.data_ptr(), B, qkv_d[:, kvd:].data_ptr(),
             qkv_d[:, 2 * kvd:].data_ptr(), f32, qkv_d.stride(0), stream),
-        "decode": lambda: lib.hs_decode(
+        "decode": lambda: lib.hs_decode_shared(
             dc.q.data_ptr(), dkc.data_ptr(), dvc.data_ptr(), kdt, dnb,
             dc.block_tables.data_ptr(), dc.context_lens.data_ptr(), dout.data_ptr(), B, H, hkv,
-            D, bs, dmb, float(dc.scale), 0, 0, ws.data_ptr(), ws_bytes, stream),
+            D, bs, dmb, float(dc.scale), 0, ws.data_ptr(), ws_bytes, stream),
         "pack": lambda: lib.hs_kv_pack(pool.data_ptr(), 1, dnb, page, ids.data_ptr(),
                                        ids.numel(), pack_out.data_ptr(), stream),
     }
@@ -332,6 +334,10 @@ def c5_step_leg(steps: int, warmup: int) -> dict:
 
     step_ms = timed(list(parts.values()))
     part_ms = {k: timed([f]) for k, f in parts.items()}
+    plain_ms = timed([lambda: lib.hs_decode(
+        dc.q.data_ptr(), dkc.data_ptr(), dvc.data_ptr(), kdt, dnb, dc.block_tables.data_ptr(),
+        dc.context_lens.data_ptr(), dout.data_ptr(), B, H, hkv, D, bs, dmb, float(dc.scale), 0,
+        0, ws.data_ptr(), ws_bytes, stream)])
     work = {
         "kv_write_chunk": ("GB/s", 2 * T * kvd * (4 + 2) / 1e9),
         "prefill": ("TFLOP/s", pc.prefill_flops() / 1e12),
@@ -347,6 +353,8 @@ def c5_step_leg(steps: int, warmup: int) -> dict:
         out["parts"][k] = {"us": round(ms * 1e3, 2), unit: round(rate, 1),
                            "frac": round(rate / peak[unit], 4)}
     out["parts"]["decode"]["basis"] = "unique K/V bytes (shared prefix counted once)"
+    out["parts"]["decode"]["path"] = "hs_decode_shared"
+    out["decode_plain_us"] = round(plain_ms * 1e3, 2)
     del dc, pc, pool, pack_out, qkv_p, qkv_d, ws
     torch.cuda.empty_cache()
     return out
@@ -499,7 +507,8 @@ def main() -> int:
         st = c5_step_leg(max(10, args.steps // 5), 10)
         secondary["C5_step"] = st
         log("C5 step: " + f"{st['us_per_step']:.1f} us = " + ", ".join(
-            f"{k} {v['us']:.1f} us" for k, v in st["parts"].items()))
+            f"{k} {v['us']:.1f} us" for k, v in st["parts"].items())
+            + f" (plain hs_decode: {st['decode_plain_us']:.1f} us)")
 
     line = {
         "metric": METRIC,

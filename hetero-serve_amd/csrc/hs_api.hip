@@ -173,11 +173,35 @@ size_t hs_decode_workspace_bytes(int B, int H, int Hkv, int D, int BS, int MB, i
   return decode_ws_bytes(B, H, D, plan.P);
 }
 
-int hs_decode(const float* q, const void* k_cache, const void* v_cache, int kv_dtype,
-              int num_blocks, const int32_t* block_tables, const int32_t* context_lens,
-              float* out, int B, int H, int Hkv, int D, int BS, int MB, float scale,
-              int num_splits, int partition_tokens, void* workspace, size_t workspace_bytes,
-              void* stream) {
+}  // extern "C"
+
+namespace hs {
+
+static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// Shared-page plan arrays after the decode workspace: skip [B * P] bytes,
+// members [P * B] int32, units [P * U] int4, unit counts [P] int32.
+struct ShareLayout {
+  size_t skip, members, units, n_units, end;
+};
+
+static ShareLayout share_layout(size_t base, int B, int P, int U) {
+  ShareLayout l;
+  l.skip = align256(base);
+  l.members = align256(l.skip + (size_t)B * P);
+  l.units = align256(l.members + (size_t)P * B * sizeof(int32_t));
+  l.n_units = align256(l.units + (size_t)P * U * 4 * sizeof(int32_t));
+  l.end = l.n_units + (size_t)P * sizeof(int32_t);
+  return l;
+}
+
+static int share_per_unit(int H, int Hkv) { return 32 / (H / Hkv); }
+
+static int decode_common(const float* q, const void* k_cache, const void* v_cache, int kv_dtype,
+                         int num_blocks, const int32_t* block_tables, const int32_t* context_lens,
+                         float* out, int B, int H, int Hkv, int D, int BS, int MB, float scale,
+                         int num_splits, int partition_tokens, void* workspace,
+                         size_t workspace_bytes, void* stream, bool shared_pages) {
   int rc = check_attn_common(q, k_cache, v_cache, kv_dtype, num_blocks, block_tables,
                              context_lens, out, B, H, Hkv, D, BS, MB);
   if (rc != HS_OK) return rc;
@@ -216,7 +240,57 @@ int hs_decode(const float* q, const void* k_cache, const void* v_cache, int kv_d
   a.splits = plan.splits;
   a.P = plan.P;
   a.qscale = scale * kLog2e;
-  return launch_row_attn(a, kv_dtype, D, static_cast<hipStream_t>(stream));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (!shared_pages || !shared_pages_apply(a, kv_dtype, D)) return launch_row_attn(a, kv_dtype, D, st);
+  SharePlanArgs sp{};
+  sp.per_unit = share_per_unit(H, Hkv);
+  sp.U = share_unit_slots(B, sp.per_unit);
+  const ShareLayout l = share_layout(need, B, plan.P, sp.U);
+  if (workspace_bytes < l.end)
+    return fail(HS_EWORKSPACE, "shared-page decode needs " + std::to_string(l.end) +
+                                   " workspace bytes, got " + std::to_string(workspace_bytes));
+  char* ws = static_cast<char*>(workspace);
+  sp.skip = reinterpret_cast<uint8_t*>(ws + l.skip);
+  sp.members = reinterpret_cast<int32_t*>(ws + l.members);
+  sp.units = reinterpret_cast<int4*>(ws + l.units);
+  sp.n_units = reinterpret_cast<int32_t*>(ws + l.n_units);
+  a.skip = sp.skip;
+  return launch_row_attn(a, kv_dtype, D, st, &sp);
+}
+
+}  // namespace hs
+
+extern "C" {
+
+int hs_decode(const float* q, const void* k_cache, const void* v_cache, int kv_dtype,
+              int num_blocks, const int32_t* block_tables, const int32_t* context_lens,
+              float* out, int B, int H, int Hkv, int D, int BS, int MB, float scale,
+              int num_splits, int partition_tokens, void* workspace, size_t workspace_bytes,
+              void* stream) {
+  return decode_common(q, k_cache, v_cache, kv_dtype, num_blocks, block_tables, context_lens,
+                       out, B, H, Hkv, D, BS, MB, scale, num_splits, partition_tokens, workspace,
+                       workspace_bytes, stream, false);
+}
+
+size_t hs_decode_shared_workspace_bytes(int B, int H, int Hkv, int D, int BS, int MB,
+                                        int partition_tokens) {
+  const size_t base = hs_decode_workspace_bytes(B, H, Hkv, D, BS, MB, 0, partition_tokens);
+  if (base == 0) return 0;   // one partition per row: nothing to share
+  DecodePlan plan;
+  if (plan_decode(BS, MB, 0, partition_tokens, default_partition(H, Hkv), &plan) != HS_OK)
+    return 0;
+  const int pu = H / Hkv <= 32 ? share_per_unit(H, Hkv) : 1;
+  return share_layout(base, B, plan.P, share_unit_slots(B, pu > 0 ? pu : 1)).end;
+}
+
+int hs_decode_shared(const float* q, const void* k_cache, const void* v_cache, int kv_dtype,
+                     int num_blocks, const int32_t* block_tables, const int32_t* context_lens,
+                     float* out, int B, int H, int Hkv, int D, int BS, int MB, float scale,
+                     int partition_tokens, void* workspace, size_t workspace_bytes,
+                     void* stream) {
+  return decode_common(q, k_cache, v_cache, kv_dtype, num_blocks, block_tables, context_lens,
+                       out, B, H, Hkv, D, BS, MB, scale, 0, partition_tokens, workspace,
+                       workspace_bytes, stream, true);
 }
 
 static int prefill_common(const float* q, const int32_t* cu_q, int S, int max_rows,

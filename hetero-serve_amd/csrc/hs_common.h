@@ -30,6 +30,7 @@ struct Elem;
 template <>
 struct Elem<float> {
   static constexpr int kVec = 4;  // elements in one 16-byte load
+  static constexpr int kCode = HS_DTYPE_F32;
   __device__ static inline void to_f32(const uint4& w, float* f) {
     f[0] = __uint_as_float(w.x);
     f[1] = __uint_as_float(w.y);
@@ -41,6 +42,7 @@ struct Elem<float> {
 template <>
 struct Elem<_Float16> {
   static constexpr int kVec = 8;
+  static constexpr int kCode = HS_DTYPE_F16;
   __device__ static inline void pair(uint32_t u, float* f) {
     typedef _Float16 h2 __attribute__((ext_vector_type(2)));
     h2 v = __builtin_bit_cast(h2, u);
@@ -63,6 +65,7 @@ struct Bf16 {
 template <>
 struct Elem<Bf16> {
   static constexpr int kVec = 8;
+  static constexpr int kCode = HS_DTYPE_BF16;
   __device__ static inline void pair(uint32_t u, float* f) {
     f[0] = __uint_as_float(u << 16);
     f[1] = __uint_as_float(u & 0xffff0000u);

@@ -57,6 +57,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void row_attn_part_kernel(RowAtt
   const int64_t rp = wg / n_groups;        // row * P + partition
   const int row = (int)(rp / a.P);
   const int p = (int)(rp - (int64_t)row * a.P);
+  if (a.skip && a.skip[rp]) return;        // served by the shared-page kernel
 
   int b, end;
   if (!row_geometry(a, row, b, end)) return;
@@ -334,7 +335,6 @@ static void launch_typed(const RowAttnArgs& a, hipStream_t stream) {
     default: launch_part<T, D, 1>(a, stream); break;
   }
   profile_end(stream);
-  if (a.P > 1) launch_merge(a, D, stream);
 }
 
 template <typename T>
@@ -351,32 +351,47 @@ static int launch_dim(const RowAttnArgs& a, int D, hipStream_t stream) {
 
 // Launch the partition kernel (+ merge when P > 1).  Arguments are validated
 // by the caller.  Grouped-query calls that the matrix-core kernel serves go
-// there (hs_decode_gqa.hip); the rest run the VALU kernel above.
-int launch_row_attn(const RowAttnArgs& a, int kv_dtype, int D, hipStream_t stream) {
-  if (gqa_mfma_applies(a, kv_dtype, D)) {
-    const int64_t gx = gqa_mfma_grid(a);
-    if (gx <= 0) return HS_OK;
-    if (gx > 0x7fffffffLL)
-      return fail(HS_EUNSUPPORTED, "grid too large: rows * partitions * head groups = " +
-                                       std::to_string(gx));
-    profile_begin(stream);
-    launch_gqa_mfma_part(a, kv_dtype, D, stream);
-    profile_end(stream);
-    if (a.P > 1) launch_merge(a, D, stream);
-    return check_launch("paged attention");
+// there (hs_decode_gqa.hip); the rest run the VALU kernel above.  With
+// `shared`: the plan kernel, then the shared-page kernel, then the partition
+// kernel (which skips the grouped partitions), then the merge.  The shared
+// kernel runs first, alone: beside the partition kernel its large workgroups
+// waited for whole CUs to drain and finished last.
+int launch_row_attn(const RowAttnArgs& a, int kv_dtype, int D, hipStream_t stream,
+                    const SharePlanArgs* shared) {
+  const bool mfma = gqa_mfma_applies(a, kv_dtype, D);
+  int64_t gx;
+  if (mfma) {
+    gx = gqa_mfma_grid(a);
+  } else {
+    const int G = row_attn_heads_per_wave(a.H, a.Hkv);
+    gx = (int64_t)a.rows * a.P * ((a.H / G + kDecodeWaves - 1) / kDecodeWaves);
   }
-  const int G = row_attn_heads_per_wave(a.H, a.Hkv);
-  const int64_t gx = (int64_t)a.rows * a.P * ((a.H / G + kDecodeWaves - 1) / kDecodeWaves);
   if (gx <= 0) return HS_OK;
   if (gx > 0x7fffffffLL)
     return fail(HS_EUNSUPPORTED, "grid too large: rows * partitions * head groups = " +
                                      std::to_string(gx));
-  switch (kv_dtype) {
-    case HS_DTYPE_F32: return launch_dim<float>(a, D, stream);
-    case HS_DTYPE_F16: return launch_dim<_Float16>(a, D, stream);
-    case HS_DTYPE_BF16: return launch_dim<Bf16>(a, D, stream);
-    default: return fail(HS_EINVAL, "unknown kv dtype code " + std::to_string(kv_dtype));
+  if (kv_dtype != HS_DTYPE_F32 && kv_dtype != HS_DTYPE_F16 && kv_dtype != HS_DTYPE_BF16)
+    return fail(HS_EINVAL, "unknown kv dtype code " + std::to_string(kv_dtype));
+  if (shared) {
+    launch_share_plan(a, *shared, stream);
+    launch_shared_pages(a, *shared, kv_dtype, D, stream);
   }
+
+  int rc = HS_OK;
+  if (mfma) {
+    profile_begin(stream);
+    launch_gqa_mfma_part(a, kv_dtype, D, stream);
+    profile_end(stream);
+  } else if (kv_dtype == HS_DTYPE_F32) {
+    rc = launch_dim<float>(a, D, stream);
+  } else if (kv_dtype == HS_DTYPE_F16) {
+    rc = launch_dim<_Float16>(a, D, stream);
+  } else {
+    rc = launch_dim<Bf16>(a, D, stream);
+  }
+  if (rc != HS_OK) return rc;
+  if (a.P > 1) launch_merge(a, D, stream);
+  return check_launch("paged attention");
 }
 
 }  // namespace hs

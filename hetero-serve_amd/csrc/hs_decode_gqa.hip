@@ -29,6 +29,11 @@
 // The partition states (m, l, un-normalised acc) have the layout and meaning
 // of the VALU kernel's, so the same merge kernel combines them.
 //
+// The same wave code serves shared pages (prefix caching, hs_decode_shared):
+// there the 32 query slots of a wave are (sequence, head) pairs of several
+// sequences whose partition has the same block ids, found on the device by
+// share_plan_kernel, so such a partition is read once for all of them.
+//
 // Used for paged caches with 16-token blocks, fixed partitions of at most
 // 1024 tokens, head_dim 32, 64 or 128 and at least 8 query heads per KV
 // head (at 4 the VALU kernel's packed heads measured faster: 169 against
@@ -61,9 +66,16 @@ struct GqaWaveLds {
   _Float16 vt[D][kBlock + kVtPad];  // V of one block, transposed
 };
 
+// One wave's partition pass: up to 32 query slots that read the same KV
+// head and the same pages, keys [lo, hi) of block table row `bt`.  Lane
+// (j, hh) serves slot j: its query starts at element q_off of a.q, and its
+// result goes either normalised to a.out at element out_off (`direct`, the
+// row's only partition) or as the partition state pi of a.part_acc /
+// a.part_ml.  Slots j >= gc are padding (zero query, nothing written).
 template <typename T, int D>
-__global__ __launch_bounds__(kGqaWaves * 64) __attribute__((amdgpu_waves_per_eu(2)))
-void gqa_mfma_part_kernel(RowAttnArgs a) {
+__device__ inline void gqa_wave_run(const RowAttnArgs& a, GqaWaveLds<D>& w, int lane, int kvh,
+                                    int gc, const int32_t* bt, int lo, int hi, int64_t q_off,
+                                    float16x (&o)[D / 32], float& m, float& l) {
   constexpr int kDC16 = D / 16;     // QK k-steps
   constexpr int kDB = D / 32;       // 32-dim output blocks
   constexpr int kDC = D / 8;        // 16-byte chunks per head row
@@ -71,52 +83,19 @@ void gqa_mfma_part_kernel(RowAttnArgs a) {
   constexpr int kLi = kBlock / kTpi;   // loads per block, for K and for V
   constexpr int kG = kLi / 2;       // consecutive V tokens per lane and page
   static_assert(kTpi <= 16 && kG >= 1, "head_dim");
-  __shared__ GqaWaveLds<D> lds[kGqaWaves];
-
-  const int lane = threadIdx.x & 63;
-  const int wv = threadIdx.x >> 6;
   const int j = lane & 31;
   const int hh = lane >> 5;
-  const int G = a.H / a.Hkv;
-  const int n_hc = (G + kHeadsPerWave - 1) / kHeadsPerWave;   // head chunks per KV head
-  const int n_units = a.Hkv * n_hc;
-  // Waves are numbered unit-fastest over (row, partition, unit), so the waves
-  // of a workgroup read neighbouring KV heads of the same tokens, and take
-  // further (row, partition) pairs when a row has fewer than kGqaWaves units.
-  const int64_t gw = (int64_t)blockIdx.x * kGqaWaves + wv;
-  if (gw >= (int64_t)a.rows * a.P * n_units) return;   // no barriers below
-  const int unit = (int)(gw % n_units);
-  const int kvh = unit / n_hc;
-  const int hc = unit - kvh * n_hc;
-  const int h0 = kvh * G + hc * kHeadsPerWave;
-  const int gc = min(kHeadsPerWave, G - hc * kHeadsPerWave);   // heads of this wave
-  const int64_t rp = gw / n_units;
-  const int row = (int)(rp / a.P);
-  const int p = (int)(rp - (int64_t)row * a.P);
-
-  int b, end;
-  if (!row_geometry(a, row, b, end)) return;
-  int lo = 0, hi = 0, nparts = 0;
-  const bool live = partition_range(a, end, p, lo, hi, nparts);
-  const int64_t orow0 = ((int64_t)row * a.H + h0) * D;
-  if (!live) {
-    if (end <= 0 && p == 0) {   // nothing to attend to: zero rows
-      for (int d = lane; d < gc * D; d += 64) a.out[orow0 + d] = 0.0f;
-    }
-    return;
-  }
 
   // Block ids of the partition's pages: lane i holds page lo / 16 + i
   // (clamped to the table); 1024 tokens are at most 64 pages.
-  const int32_t* bt = a.bt + (int64_t)b * a.MB;
   const int page0 = lo >> 4;
   const int idv = bt[min(page0 + lane, a.MB - 1)];
 
-  // Q^T fragments: lane (j, hh) holds head h0 + j, dims 16c + 8hh .. +7.
+  // Q^T fragments: lane (j, hh) holds slot j, dims 16c + 8hh .. +7.
   half8 qf[kDC16];
   {
     const float sc = j < gc ? a.qscale : 0.0f;
-    const float* qp = a.q + orow0 + (int64_t)min(j, gc - 1) * D + 8 * hh;
+    const float* qp = a.q + q_off + 8 * hh;
 #pragma unroll
     for (int c = 0; c < kDC16; ++c) {
       const float4 x0 = *reinterpret_cast<const float4*>(qp + 16 * c);
@@ -126,7 +105,6 @@ void gqa_mfma_part_kernel(RowAttnArgs a) {
                             pack_f16(x1.x * sc, x1.y * sc), pack_f16(x1.z * sc, x1.w * sc)));
     }
   }
-
   const int64_t tok = (int64_t)a.Hkv * D;           // elements between tokens of a page
   // Loads are coalesced: kDC neighbouring lanes read one token's head row.
   // Lane L holds chunk L % kDC of token slot L / kDC.  K load u covers
@@ -181,14 +159,12 @@ void gqa_mfma_part_kernel(RowAttnArgs a) {
       }
   };
 
-  float16x o[kDB];
 #pragma unroll
   for (int d = 0; d < kDB; ++d)
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[d][r] = 0.0f;
-  float m = kNegBig;   // running max of head j (shared by lanes j, j + 32)
-  float l = 0.0f;      // this lane's share of the running sum
-  GqaWaveLds<D>& w = lds[wv];
+  m = kNegBig;   // running max of head j (shared by lanes j, j + 32)
+  l = 0.0f;      // this lane's share of the running sum
 
   load_block(0);
   for (int t0 = lo; t0 < hi; t0 += kBlock) {
@@ -247,12 +223,21 @@ void gqa_mfma_part_kernel(RowAttnArgs a) {
       }
   }
 
-  // Partition state of head h0 + j: lane (j, hh) owns dims d*32 + 8g + 4hh + 0..3.
+}
+
+// Result of slot j of a wave: lane (j, hh) owns dims d*32 + 8g + 4hh + 0..3.
+template <int D>
+__device__ inline void gqa_wave_store(const RowAttnArgs& a, int lane, int gc,
+                                      const float16x (&o)[D / 32], float m, float l, bool direct,
+                                      int64_t out_off, int64_t pi) {
+  constexpr int kDB = D / 32;
+  const int j = lane & 31;
+  const int hh = lane >> 5;
   const float lsum = sum_halves(l);
   if (j >= gc) return;
-  if (nparts == 1) {
+  if (direct) {
     const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
-    float* op = a.out + orow0 + (int64_t)j * D + 4 * hh;
+    float* op = a.out + out_off + 4 * hh;
 #pragma unroll
     for (int d = 0; d < kDB; ++d)
 #pragma unroll
@@ -261,7 +246,6 @@ void gqa_mfma_part_kernel(RowAttnArgs a) {
             make_float4(o[d][4 * g] * inv, o[d][4 * g + 1] * inv, o[d][4 * g + 2] * inv,
                         o[d][4 * g + 3] * inv);
   } else {
-    const int64_t pi = ((int64_t)row * a.H + h0 + j) * a.P + p;
     float* op = a.part_acc + pi * D + 4 * hh;
 #pragma unroll
     for (int d = 0; d < kDB; ++d)
@@ -271,6 +255,57 @@ void gqa_mfma_part_kernel(RowAttnArgs a) {
             make_float4(o[d][4 * g], o[d][4 * g + 1], o[d][4 * g + 2], o[d][4 * g + 3]);
     if (hh == 0) *reinterpret_cast<float2*>(a.part_ml + 2 * pi) = make_float2(m, lsum);
   }
+}
+
+template <typename T, int D>
+__device__ inline void gqa_wave(const RowAttnArgs& a, GqaWaveLds<D>& w, int lane, int kvh, int gc,
+                                const int32_t* bt, int lo, int hi, int64_t q_off, bool direct,
+                                int64_t out_off, int64_t pi) {
+  float16x o[D / 32];
+  float m, l;
+  gqa_wave_run<T, D>(a, w, lane, kvh, gc, bt, lo, hi, q_off, o, m, l);
+  gqa_wave_store<D>(a, lane, gc, o, m, l, direct, out_off, pi);
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(kGqaWaves * 64) __attribute__((amdgpu_waves_per_eu(2)))
+void gqa_mfma_part_kernel(RowAttnArgs a) {
+  __shared__ GqaWaveLds<D> lds[kGqaWaves];
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  const int j = lane & 31;
+  const int G = a.H / a.Hkv;
+  const int n_hc = (G + kHeadsPerWave - 1) / kHeadsPerWave;   // head chunks per KV head
+  const int n_units = a.Hkv * n_hc;
+  // Waves are numbered unit-fastest over (row, partition, unit), so the waves
+  // of a workgroup read neighbouring KV heads of the same tokens, and take
+  // further (row, partition) pairs when a row has fewer than kGqaWaves units.
+  const int64_t gw = (int64_t)blockIdx.x * kGqaWaves + wv;
+  if (gw >= (int64_t)a.rows * a.P * n_units) return;   // no barriers below
+  const int unit = (int)(gw % n_units);
+  const int kvh = unit / n_hc;
+  const int hc = unit - kvh * n_hc;
+  const int h0 = kvh * G + hc * kHeadsPerWave;
+  const int gc = min(kHeadsPerWave, G - hc * kHeadsPerWave);   // heads of this wave
+  const int64_t rp = gw / n_units;
+  const int row = (int)(rp / a.P);
+  const int p = (int)(rp - (int64_t)row * a.P);
+  if (a.skip && a.skip[rp]) return;   // served by the shared-page kernel
+
+  int b, end;
+  if (!row_geometry(a, row, b, end)) return;
+  int lo = 0, hi = 0, nparts = 0;
+  const bool live = partition_range(a, end, p, lo, hi, nparts);
+  const int64_t orow0 = ((int64_t)row * a.H + h0) * D;
+  if (!live) {
+    if (end <= 0 && p == 0) {   // nothing to attend to: zero rows
+      for (int d = lane; d < gc * D; d += 64) a.out[orow0 + d] = 0.0f;
+    }
+    return;
+  }
+  gqa_wave<T, D>(a, lds[wv], lane, kvh, gc, a.bt + (int64_t)b * a.MB, lo, hi,
+                 orow0 + (int64_t)min(j, gc - 1) * D, nparts == 1, orow0 + (int64_t)j * D,
+                 ((int64_t)row * a.H + h0 + j) * a.P + p);
 }
 
 int64_t grid_size(const RowAttnArgs& a) {
@@ -285,6 +320,234 @@ void launch_typed(const RowAttnArgs& a, hipStream_t stream) {
                      dim3(kGqaWaves * 64), 0, stream, a);
 }
 
+// ---------------------------------------------------------------------------
+// Shared pages (prefix caching): sequences whose full partition p has the
+// same block ids read the same K/V.  The plan kernel groups them; one wave of
+// the shared-page kernel then serves up to 32 query slots, (sequence, head)
+// pairs of one KV head, with gqa_wave, reading the pages once.
+// ---------------------------------------------------------------------------
+
+constexpr int kShareMaxB = 2048;   // sequences the plan kernel can group
+constexpr int kShareMin = 4;       // sequences that must hold a partition to group it
+
+constexpr int kShareMaxPages = 64; // pages of a partition (1024 tokens)
+
+// The n (>= 1) block ids from entry `first` of a table row of MB entries,
+// all loads issued at once and unconditionally (a load under a condition
+// makes the compiler wait for every earlier one): entries past n repeat id
+// n - 1, and indices are clamped to the row.
+__device__ inline void load_ids(const int32_t* row, int first, int n, int MB,
+                                int32_t (&v)[kShareMaxPages]) {
+#pragma unroll
+  for (int i = 0; i < kShareMaxPages; ++i) v[i] = row[min(first + min(i, n - 1), MB - 1)];
+}
+
+// 64-bit FNV-1a over the ids (equal hashes are then compared id by id, so a
+// collision only costs a comparison).
+__device__ inline uint64_t ids_hash(const int32_t (&v)[kShareMaxPages], int n) {
+  uint64_t h = 1469598103934665603ull;
+#pragma unroll
+  for (int i = 0; i < kShareMaxPages; ++i)
+    if (i < n) h = (h ^ (uint32_t)v[i]) * 1099511628211ull;
+  return h;
+}
+
+// One workgroup per partition index p.  A sequence's partition p is a
+// candidate when it is full (all part_tokens keys below its context).  Its
+// representative is the first sequence with the same hash, confirmed id by
+// id (a hash collision leaves the sequence on its own).  Groups of at least
+// kShareMin sequences are laid out in members[] in sequence order and cut
+// into units of per_unit sequences.  Every scan over the batch is a
+// branch-free sum or minimum, so its LDS reads pipeline.
+__global__ __launch_bounds__(256) void share_plan_kernel(RowAttnArgs a, SharePlanArgs s) {
+  __shared__ uint64_t hsh[kShareMaxB];
+  __shared__ int rep[kShareMaxB];
+  __shared__ int cnt[kShareMaxB];
+  __shared__ int grp[kShareMaxB];    // members of the group b represents (0: none)
+  __shared__ int nun[kShareMaxB];    // units of that group
+  __shared__ int units_sum;
+  const int p = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int pages = a.part_tokens / 16;
+  const int64_t cap = (int64_t)a.MB * a.BS;
+  if (tid == 0) units_sum = 0;
+  for (int b = tid; b < a.B; b += 256) {
+    const int64_t end = a.ctx[b] < cap ? a.ctx[b] : cap;
+    const bool full = (int64_t)(p + 1) * a.part_tokens <= end;
+    int32_t v[kShareMaxPages];
+    load_ids(a.bt + (int64_t)b * a.MB, p * pages, pages, a.MB, v);
+    hsh[b] = full ? ids_hash(v, pages) : ~0ull;
+    cnt[b] = 0;
+  }
+  __syncthreads();
+  for (int b = tid; b < a.B; b += 256) {
+    int r = -1;
+    const uint64_t hb = hsh[b];
+    if (hb != ~0ull) {
+      r = b;
+#pragma unroll 8
+      for (int c = 0; c < b; ++c) r = (hsh[c] == hb && c < r) ? c : r;
+      if (r != b) {
+        int32_t mine[kShareMaxPages], other[kShareMaxPages];
+        load_ids(a.bt + (int64_t)b * a.MB, p * pages, pages, a.MB, mine);
+        load_ids(a.bt + (int64_t)r * a.MB, p * pages, pages, a.MB, other);
+        bool same = true;
+#pragma unroll
+        for (int i = 0; i < kShareMaxPages; ++i) same = same && mine[i] == other[i];
+        if (!same) r = b;
+      }
+    }
+    rep[b] = r;
+  }
+  __syncthreads();
+  // a collision can leave a sequence whose representative kept another
+  // representative: only sequences whose representative represents itself
+  // are counted
+  for (int b = tid; b < a.B; b += 256) {
+    const int r = rep[b];
+    if (r >= 0 && rep[r] == r) atomicAdd(&cnt[r], 1);
+  }
+  __syncthreads();
+  int my_units = 0;
+  for (int b = tid; b < a.B; b += 256) {
+    const bool g = rep[b] == b && cnt[b] >= kShareMin;
+    grp[b] = g ? cnt[b] : 0;
+    nun[b] = g ? (cnt[b] + s.per_unit - 1) / s.per_unit : 0;
+    my_units += nun[b];
+  }
+  __syncthreads();
+  for (int b = tid; b < a.B; b += 256) {
+    const int r = rep[b];
+    const bool grouped = r >= 0 && grp[r] > 0;
+    s.skip[(int64_t)b * a.P + p] = grouped ? 1 : 0;
+    if (!grouped) continue;
+    // members[] offset and unit offset of the group: sums over the groups of
+    // lower representatives; index of b inside its group
+    int off = 0, uoff = 0, idx = 0;
+#pragma unroll 8
+    for (int c = 0; c < r; ++c) {
+      off += grp[c];
+      uoff += nun[c];
+    }
+#pragma unroll 8
+    for (int c = r; c < b; ++c) idx += rep[c] == r;
+    s.members[(int64_t)p * a.B + off + idx] = b;
+    if (b == r) {
+      const int n = grp[r];
+      for (int k = 0; k < nun[r]; ++k)
+        s.units[(int64_t)p * s.U + uoff + k] =
+            make_int4(off + k * s.per_unit, min(s.per_unit, n - k * s.per_unit), r, 0);
+    }
+  }
+  if (my_units) atomicAdd(&units_sum, my_units);
+  __syncthreads();
+  if (tid == 0) s.n_units[p] = units_sum;
+}
+
+constexpr int kShareGroups = 256;   // workgroups of the shared-page grid
+
+// A fixed grid of workgroups strides over the work items (partition, unit,
+// KV head), KV head fastest; each prefix of partitions' unit counts comes
+// from n_units (partitions are at most 64: one per lane).  Slot j of a unit
+// is member j / G of the group with query head kvh * G + j % G.  The four
+// waves of a workgroup take a quarter of the partition's keys each, and
+// their states are combined through LDS, so that a shared partition costs a
+// quarter of a wave's walk of it.  The grid is one wave per SIMD, so the
+// kernel may use the whole register file of one.
+template <typename T, int D>
+__global__ __launch_bounds__(kGqaWaves * 64) __attribute__((amdgpu_waves_per_eu(1)))
+void shared_pages_kernel(RowAttnArgs a, SharePlanArgs s) {
+  constexpr int kDB = D / 32;
+  constexpr int kState = 16 * kDB + 2;           // floats per lane: o, m, l
+  static_assert(kState * 64 * sizeof(float) <= sizeof(GqaWaveLds<D>), "state exchange");
+  __shared__ GqaWaveLds<D> lds[kGqaWaves];
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  const int j = lane & 31;
+  int pre = lane < a.P ? s.n_units[lane] : 0;   // inclusive prefix over partitions
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int x = __shfl_up(pre, off);
+    if (lane >= off) pre += x;
+  }
+  const int total = __shfl(pre, 63);
+  const int G = a.H / a.Hkv;
+  const int64_t cap = (int64_t)a.MB * a.BS;
+  const int span = a.part_tokens / kGqaWaves / 16 * 16;   // keys per wave, page-aligned
+  // Slot j of work item `item`: its unit, member sequence and query row
+  // (recomputed after the key walk rather than held through it).
+  struct Slot {
+    int p, kvh, gc, mb;
+    int4 un;
+    int64_t row_h;
+  };
+  auto slot_of = [&](int item) {
+    Slot t;
+    t.kvh = item % a.Hkv;
+    const int k = item / a.Hkv;                  // unit number over all partitions
+    t.p = __popcll(__builtin_amdgcn_ballot_w64(lane < a.P && pre <= k));
+    const int u = k - (t.p > 0 ? __shfl(pre, t.p - 1) : 0);
+    t.un = s.units[(int64_t)t.p * s.U + u];
+    t.gc = t.un.y * G;
+    const int js = min(j, t.gc - 1);
+    t.mb = s.members[(int64_t)t.p * a.B + t.un.x + js / G];
+    t.row_h = (int64_t)t.mb * a.H + t.kvh * G + js % G;
+    return t;
+  };
+  for (int item = blockIdx.x; item < total * a.Hkv; item += gridDim.x) {   // workgroup-uniform
+    float16x o[kDB];
+    float m, l;
+    {
+      const Slot t = slot_of(item);
+      const int lo = t.p * a.part_tokens + wv * span;
+      const int hi = wv == kGqaWaves - 1 ? (t.p + 1) * a.part_tokens : lo + span;
+      gqa_wave_run<T, D>(a, lds[wv], lane, t.kvh, t.gc, a.bt + (int64_t)t.un.z * a.MB, lo, hi,
+                         t.row_h * D, o, m, l);
+    }
+    __syncthreads();   // every wave is done with its K/V tiles
+    float* xs = reinterpret_cast<float*>(&lds[wv]);
+    if (wv > 0) {
+#pragma unroll
+      for (int d = 0; d < kDB; ++d)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) xs[(16 * d + r) * 64 + lane] = o[d][r];
+      xs[16 * kDB * 64 + lane] = m;
+      xs[(16 * kDB + 1) * 64 + lane] = l;
+    }
+    __syncthreads();
+    if (wv == 0) {
+      float mm = m;
+#pragma unroll
+      for (int w = 1; w < kGqaWaves; ++w)
+        mm = fmaxf(mm, reinterpret_cast<const float*>(&lds[w])[16 * kDB * 64 + lane]);
+      const float c0 = fast_exp2(m - mm);
+      l *= c0;
+#pragma unroll
+      for (int d = 0; d < kDB; ++d)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[d][r] *= c0;
+#pragma unroll
+      for (int w = 1; w < kGqaWaves; ++w) {
+        // one wave's state at a time (the fence keeps the scheduler from
+        // loading all of them ahead of the sums)
+        __builtin_amdgcn_sched_barrier(0);
+        const float* xw = reinterpret_cast<const float*>(&lds[w]);
+        const float cw = fast_exp2(xw[16 * kDB * 64 + lane] - mm);
+        l += cw * xw[(16 * kDB + 1) * 64 + lane];
+#pragma unroll
+        for (int d = 0; d < kDB; ++d)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) o[d][r] += cw * xw[(16 * d + r) * 64 + lane];
+      }
+      const Slot t = slot_of(item);
+      const int64_t end = a.ctx[t.mb] < cap ? a.ctx[t.mb] : cap;
+      gqa_wave_store<D>(a, lane, t.gc, o, mm, l, end <= a.part_tokens, t.row_h * D,
+                        t.row_h * a.P + t.p);
+    }
+    __syncthreads();   // the exchange area is free for the next item
+  }
+}
+
 }  // namespace
 
 bool gqa_mfma_applies(const RowAttnArgs& a, int kv_dtype, int D) {
@@ -294,6 +557,41 @@ bool gqa_mfma_applies(const RowAttnArgs& a, int kv_dtype, int D) {
 }
 
 int64_t gqa_mfma_grid(const RowAttnArgs& a) { return grid_size(a); }
+
+bool shared_pages_apply(const RowAttnArgs& a, int kv_dtype, int D) {
+  const int G = a.H / a.Hkv;
+  return (kv_dtype == HS_DTYPE_F16 || kv_dtype == HS_DTYPE_BF16) && a.BS == 16 &&
+         (D == 32 || D == 64 || D == 128) && a.mode == 1 && a.part_tokens <= 16 * kShareMaxPages &&
+         a.P > 1 && a.P <= 64 && G <= kHeadsPerWave / 2 && a.B <= kShareMaxB &&
+         a.cu_q == nullptr &&
+         a.S == 1;
+}
+
+int share_unit_slots(int B, int per_unit) {
+  return (B + kShareMin - 1) / kShareMin + (B + per_unit - 1) / per_unit;
+}
+
+void launch_share_plan(const RowAttnArgs& a, const SharePlanArgs& s, hipStream_t stream) {
+  hipLaunchKernelGGL(share_plan_kernel, dim3((unsigned)a.P), dim3(256), 0, stream, a, s);
+}
+
+void launch_shared_pages(const RowAttnArgs& a, const SharePlanArgs& s, int kv_dtype, int D,
+                         hipStream_t stream) {
+  const dim3 grid(kShareGroups), block(kGqaWaves * 64);
+  if (kv_dtype == HS_DTYPE_F16) {
+    switch (D) {
+      case 32: hipLaunchKernelGGL((shared_pages_kernel<_Float16, 32>), grid, block, 0, stream, a, s); break;
+      case 64: hipLaunchKernelGGL((shared_pages_kernel<_Float16, 64>), grid, block, 0, stream, a, s); break;
+      default: hipLaunchKernelGGL((shared_pages_kernel<_Float16, 128>), grid, block, 0, stream, a, s); break;
+    }
+  } else {
+    switch (D) {
+      case 32: hipLaunchKernelGGL((shared_pages_kernel<Bf16, 32>), grid, block, 0, stream, a, s); break;
+      case 64: hipLaunchKernelGGL((shared_pages_kernel<Bf16, 64>), grid, block, 0, stream, a, s); break;
+      default: hipLaunchKernelGGL((shared_pages_kernel<Bf16, 128>), grid, block, 0, stream, a, s); break;
+    }
+  }
+}
 
 void launch_gqa_mfma_part(const RowAttnArgs& a, int kv_dtype, int D, hipStream_t stream) {
   if (kv_dtype == HS_DTYPE_F16) {

@@ -26,6 +26,7 @@ struct RowAttnArgs {
   int splits;             // mode 2
   int P;                  // partition slots per (row, head) in the grid
   float qscale;           // scale * log2(e)
+  const uint8_t* skip;    // [rows * P] or null: partitions the shared-page kernel serves
 };
 
 // Sequence of a row and the end of its key range (exclusive).  Returns false
@@ -76,7 +77,29 @@ __device__ inline bool partition_range(const RowAttnArgs& a, int end, int p, int
 void profile_begin(hipStream_t stream);
 void profile_end(hipStream_t stream);
 
-int launch_row_attn(const RowAttnArgs& a, int kv_dtype, int D, hipStream_t stream);
+// Shared-page decode (hs_decode_shared): where the block ids of a full
+// partition are the same in several sequences (prefix caching), the plan
+// kernel groups those sequences and a matrix-core kernel reads the pages once
+// for up to 32 query slots; the partition kernel skips the grouped
+// (sequence, partition) pairs.  Device arrays, in the caller's workspace.
+struct SharePlanArgs {
+  uint8_t* skip;       // [B * P]  1: (b, p) served by the shared-page kernel
+  int32_t* members;    // [P * B]  per partition: the grouped sequences, group by group
+  int4* units;         // [P * U]  (first member, members, representative sequence, 0)
+  int32_t* n_units;    // [P]
+  int U;               // unit slots per partition
+  int per_unit;        // sequences per unit (32 query slots / G heads per KV head)
+};
+bool shared_pages_apply(const RowAttnArgs& a, int kv_dtype, int D);
+int share_unit_slots(int B, int per_unit);
+void launch_share_plan(const RowAttnArgs& a, const SharePlanArgs& s, hipStream_t stream);
+void launch_shared_pages(const RowAttnArgs& a, const SharePlanArgs& s, int kv_dtype, int D,
+                         hipStream_t stream);
+
+// Partition kernel + merge; with `shared`, the plan kernel before and the
+// shared-page kernel between them.
+int launch_row_attn(const RowAttnArgs& a, int kv_dtype, int D, hipStream_t stream,
+                    const SharePlanArgs* shared = nullptr);
 
 // Grouped-query partition kernel on the matrix cores (hs_decode_gqa.hip):
 // whether it serves this call, its grid size, and its launch (the merge of

@@ -22,7 +22,7 @@ import threading
 from pathlib import Path
 from typing import Optional
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
 
 _lock = threading.Lock()
@@ -44,6 +44,10 @@ _SIGNATURES = {
     "hs_decode": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_vp, _c_vp, _c_vp,
                            _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float,
                            _c_int, _c_int, _c_vp, _c_size, _c_vp]),
+    "hs_decode_shared_workspace_bytes": (_c_size, [_c_int] * 7),
+    "hs_decode_shared": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_vp, _c_vp, _c_vp,
+                                  _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float,
+                                  _c_int, _c_vp, _c_size, _c_vp]),
     "hs_prefill_workspace_bytes": (_c_size, [_c_int] * 5),
     "hs_prefill": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_vp, _c_vp, _c_vp,
                             _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
@@ -220,8 +224,12 @@ class _DeviceGuard:
 
 
 def decode(q, k_cache, v_cache, block_tables, context_lens, scale: float,
-           num_splits: int, partition_tokens: int = 0):
-    """out[B, H, D] fp32 = paged decode attention via hs_decode."""
+           num_splits: int, partition_tokens: int = 0, shared_pages: bool = False):
+    """out[B, H, D] fp32 = paged decode attention via hs_decode.
+
+    shared_pages=True (fixed partitions only, num_splits == 0) runs
+    hs_decode_shared: partitions whose block ids several sequences share are
+    read once for all of them."""
     import torch
 
     L = lib()
@@ -242,15 +250,28 @@ def decode(q, k_cache, v_cache, block_tables, context_lens, scale: float,
     out = torch.empty((B, H, D), dtype=torch.float32, device=q.device)
     if B == 0:
         return out
-    ws_bytes = L.hs_decode_workspace_bytes(B, H, Hkv, D, BS, max(MB, 1), int(num_splits),
-                                           int(partition_tokens))
+    if shared_pages and int(num_splits) != 0:
+        raise RuntimeError("shared_pages needs fixed partitions (num_splits == 0)")
+    if shared_pages:
+        ws_bytes = L.hs_decode_shared_workspace_bytes(B, H, Hkv, D, BS, max(MB, 1),
+                                                      int(partition_tokens))
+    else:
+        ws_bytes = L.hs_decode_workspace_bytes(B, H, Hkv, D, BS, max(MB, 1), int(num_splits),
+                                               int(partition_tokens))
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes else None
+    wsp = ws.data_ptr() if ws is not None else None
     with _DeviceGuard(q.device):
-        check(L.hs_decode(
-            q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), dtype_code(k_cache.dtype),
-            NB, bt.data_ptr(), ctx.data_ptr(), out.data_ptr(), B, H, Hkv, D, BS, MB,
-            float(scale), int(num_splits), int(partition_tokens),
-            ws.data_ptr() if ws is not None else None, ws_bytes, stream_of(q.device)))
+        if shared_pages:
+            check(L.hs_decode_shared(
+                q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), dtype_code(k_cache.dtype),
+                NB, bt.data_ptr(), ctx.data_ptr(), out.data_ptr(), B, H, Hkv, D, BS, MB,
+                float(scale), int(partition_tokens), wsp, ws_bytes, stream_of(q.device)))
+        else:
+            check(L.hs_decode(
+                q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), dtype_code(k_cache.dtype),
+                NB, bt.data_ptr(), ctx.data_ptr(), out.data_ptr(), B, H, Hkv, D, BS, MB,
+                float(scale), int(num_splits), int(partition_tokens), wsp, ws_bytes,
+                stream_of(q.device)))
     return out
 
 

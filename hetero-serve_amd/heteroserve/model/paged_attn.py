@@ -50,6 +50,13 @@ def build_error() -> Optional[str]:
     return _hip.error()
 
 
-def paged_attention(q, k_cache, v_cache, block_tables, context_lens, scale):
-    """Decode attention over the paged pool on the GPU (raises when unavailable)."""
-    return _hip.decode(q, k_cache, v_cache, block_tables, context_lens, scale, num_splits=0)
+def paged_attention(q, k_cache, v_cache, block_tables, context_lens, scale,
+                    shared_pages: bool = False):
+    """Decode attention over the paged pool on the GPU (raises when unavailable).
+
+    shared_pages (not in the reference's signature, default off): for batches
+    whose sequences share cached prefix pages, read a partition that several
+    sequences hold once for all of them (hs_decode_shared; same function,
+    fp16 matrix-core operands on the shared partitions)."""
+    return _hip.decode(q, k_cache, v_cache, block_tables, context_lens, scale, num_splits=0,
+                       shared_pages=shared_pages)

@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define HS_ABI_VERSION 3
+#define HS_ABI_VERSION 4
 
 /* KV element type codes (the pool dtype). */
 #define HS_DTYPE_F32 0
@@ -121,6 +121,31 @@ int hs_decode(const float* q, const void* k_cache, const void* v_cache, int kv_d
               float* out, int B, int H, int Hkv, int D, int BS, int MB, float scale,
               int num_splits, int partition_tokens, void* workspace,
               size_t workspace_bytes, void* stream);
+
+/*
+ * Decode for batches whose sequences share pages (prefix caching: the same
+ * block ids at the same positions of several block tables).  Computes what
+ * hs_decode(num_splits = 0, partition_tokens) computes.  A partition of
+ * partition_tokens keys that is full in at least 4 sequences with identical
+ * block ids is read once for up to 32 (sequence, head) query slots of a KV
+ * head on the matrix cores (fp16 operands, fp32 accumulation: within 1e-3 of
+ * the fp32 path, like the grouped-query matrix-core decode); every other
+ * partition runs as in hs_decode.  The grouping is found on the device by
+ * one small kernel per call.  Serves fp16/bf16 KV with BS == 16, D in
+ * {32, 64, 128}, partitions of at most 1024 tokens, at most 16 query heads per
+ * KV head and B <= 2048; other calls run hs_decode's path unchanged.
+ * No reference counterpart (the reference reads every sequence's pages);
+ * version 4 of the ABI added it.
+ *   workspace  device scratch of hs_decode_shared_workspace_bytes(...) bytes
+ *              (hs_decode's partition states plus the grouping).
+ */
+size_t hs_decode_shared_workspace_bytes(int B, int H, int Hkv, int D, int BS, int MB,
+                                        int partition_tokens);
+int hs_decode_shared(const float* q, const void* k_cache, const void* v_cache, int kv_dtype,
+                     int num_blocks, const int32_t* block_tables, const int32_t* context_lens,
+                     float* out, int B, int H, int Hkv, int D, int BS, int MB, float scale,
+                     int partition_tokens, void* workspace, size_t workspace_bytes,
+                     void* stream);
 
 /*
  * Workspace bytes hs_prefill / hs_prefill_varlen may use for B sequences of

@@ -40,7 +40,7 @@ def test_header_declarations_are_bound_by_the_loader():
 def test_library_exports_every_declared_symbol(lib):
     for name in _declared_functions():
         assert hasattr(lib, name), name
-    assert lib.hs_abi_version() == 3
+    assert lib.hs_abi_version() == 4
     assert lib.hs_last_error() == b""
 
 
@@ -68,6 +68,13 @@ def test_argument_errors_need_no_device(lib):
     assert rc == -4 and b"workspace" in lib.hs_last_error()
     assert lib.hs_decode_workspace_bytes(2, 4, 4, 64, 16, 64, 1, 0) == 0      # one pass
     assert lib.hs_decode_workspace_bytes(2, 4, 4, 64, 16, 64, 0, 24) == 0     # bad partition
+    # shared-page decode: hs_decode's partition states plus the grouping arrays
+    base = lib.hs_decode_workspace_bytes(255, 32, 32, 128, 16, 256, 0, 0)
+    assert lib.hs_decode_shared_workspace_bytes(255, 32, 32, 128, 16, 256, 0) > base > 0
+    assert lib.hs_decode_shared_workspace_bytes(4, 32, 32, 128, 16, 32, 0) == 0   # one partition
+    rc = lib.hs_decode_shared(fake, fake, fake, 0, 8, fake, fake, fake, 1, 6, 4, 64, 16, 2,
+                              0.1, 0, None, 0, None)
+    assert rc == -1 and b"divisible" in lib.hs_last_error()
     assert lib.hs_prefill_workspace_bytes(1, 1024, 32, 128, 0) == 0          # row kernel
     assert lib.hs_prefill_workspace_bytes(0, 1024, 32, 128, 1) == 0          # nothing to do
     rc = lib.hs_prefill(fake, fake, fake, 0, 8, fake, fake, fake, 1, 4, 4, 4, 64, 16, 2,

@@ -359,3 +359,119 @@ def test_large_configs(name):
     assert torch.isfinite(fast).all()
     del case
     torch.cuda.empty_cache()
+
+
+# ---------------------------------------------------------------------------
+# shared pages (prefix caching): hs_decode_shared
+# ---------------------------------------------------------------------------
+
+
+def _shared_pages_case(ctx, groups, H, Hkv, D, dtype, seed):
+    """Block tables where each group (members, n_blocks) starts with the same
+    n_blocks block ids; every other page is private.  Pool filled from N(0, 1)."""
+    rng = np.random.default_rng(seed)
+    need = [-(-int(n) // 16) for n in ctx]
+    nb = sum(need) + 16
+    perm = iter(rng.permutation(nb).tolist())
+    prefix_of = {}
+    for members, n_blocks in groups:
+        ids = [next(perm) for _ in range(n_blocks)]
+        for b in members:
+            prefix_of[b] = ids
+    tables = []
+    for b, n in enumerate(need):
+        t = list(prefix_of.get(b, [])[:n])
+        while len(t) < n:
+            t.append(next(perm))
+        tables.append(t)
+    gen = torch.Generator(device=DEV).manual_seed(seed)
+    pool = torch.randn((nb, 16, Hkv, D), generator=gen, device=DEV).to(dtype)
+    vpool = torch.randn((nb, 16, Hkv, D), generator=gen, device=DEV).to(dtype)
+    q = torch.randn((len(ctx), H, D), generator=gen, device=DEV)
+    width = max(need)
+    bt = torch.full((len(ctx), width), -1, dtype=torch.int32)
+    for b, t in enumerate(tables):
+        bt[b, :len(t)] = torch.tensor(t, dtype=torch.int32)
+    return (q, pool, vpool, bt.to(DEV), torch.tensor(ctx, dtype=torch.int32, device=DEV),
+            D ** -0.5)
+
+
+def _oracle_rows(q, kc, vc, bt, ctx, scale, rows):
+    out = {}
+    for b in rows:
+        n = int(ctx[b])
+        nblk = -(-n // 16)
+        blocks = bt[b, :nblk].long()
+        out[b] = decode_one(q[b].cpu(), kc.index_select(0, blocks).cpu(),
+                            vc.index_select(0, blocks).cpu(),
+                            torch.arange(nblk, dtype=torch.int32), n, scale)
+    return out
+
+
+@pytest.mark.parametrize("H,Hkv,D,dtype,pt,ctx,groups", [
+    # a group of 8 over 1024 tokens (members at 512 tokens have only that
+    # partition, members below 1024 share partition 0 only), a pair (too few
+    # to group), a group of exactly 4 over one partition, private sequences
+    (8, 8, 128, torch.bfloat16, 0,
+     [1024, 1100, 1536, 2000, 530, 512, 1031, 4000, 1500, 1700, 600, 777, 513, 640, 90, 3000],
+     [(range(0, 8), 64), ([8, 9], 96), ([10, 11, 12, 13], 40)]),
+    # GQA, 4 query heads per KV head: 8 sequences per unit, 40 sharers
+    (16, 4, 64, torch.float16, 0, [2048 + 37 * i for i in range(40)] + [700, 3000],
+     [(range(0, 40), 128)]),
+    # 70 sharers of 256-token partitions: units of 32, 32 and 6
+    (4, 4, 32, torch.bfloat16, 256, [1300 + 11 * i for i in range(70)], [(range(0, 70), 80)]),
+])
+def test_shared_pages_decode(H, Hkv, D, dtype, pt, ctx, groups):
+    """Sequences holding the same pages: their shared partitions are read once
+    for the whole group on the matrix cores.  Every sequence against the
+    per-sequence oracle at 2e-3; outputs of sequences in no group are the
+    plain path's, bit for bit."""
+    from heteroserve import _hip
+
+    _mods()
+    q, kc, vc, bt, cl, scale = _shared_pages_case(ctx, groups, H, Hkv, D, dtype, seed=len(ctx))
+    plain = _hip.decode(q, kc, vc, bt, cl, scale, num_splits=0, partition_tokens=pt)
+    shared = _hip.decode(q, kc, vc, bt, cl, scale, num_splits=0, partition_tokens=pt,
+                         shared_pages=True)
+    assert torch.isfinite(shared).all()
+    want = _oracle_rows(q, kc, vc, bt, cl, scale, range(len(ctx)))
+    for b, w in want.items():
+        err = _maxerr(shared[b], w)
+        assert err <= 2e-3, f"sequence {b} ctx {ctx[b]}: {err:.2e}"
+    grouped = {b for members, _ in groups if len(members) >= 4 for b in members}
+    for b in range(len(ctx)):
+        if b not in grouped:
+            assert torch.equal(shared[b], plain[b]), b
+
+
+def test_shared_pages_c5():
+    """C5's decode batch (half the sequences share a 1024-token prefix):
+    the shared-page path against the plain one and sampled sequences against
+    the oracle, 2e-3."""
+    from heteroserve import _hip
+
+    _mods()
+    case = _config("C5-decode")
+    args = (case.q, case.k_cache, case.v_cache, case.block_tables, case.context_lens,
+            case.scale)
+    plain = _hip.decode(*args, num_splits=0)
+    shared = _hip.decode(*args, num_splits=0, shared_pages=True)
+    assert _maxerr(shared, plain) <= 2e-3
+    _check_sequences(case, shared, [0, 1, 2, 3, 100, 200, 254], 2e-3)
+    del case
+    torch.cuda.empty_cache()
+
+
+def test_shared_pages_fallbacks():
+    """Geometries the shared-page kernel does not serve run hs_decode's path:
+    fp32 pools give the plain result bit for bit; num_splits != 0 is refused."""
+    from heteroserve import _hip
+
+    _mods()
+    q, kc, vc, bt, cl, scale = _shared_pages_case([1024] * 6, [(range(6), 64)], 4, 4, 64,
+                                                  torch.float32, seed=3)
+    plain = _hip.decode(q, kc, vc, bt, cl, scale, num_splits=0)
+    shared = _hip.decode(q, kc, vc, bt, cl, scale, num_splits=0, shared_pages=True)
+    assert torch.equal(plain, shared)
+    with pytest.raises(RuntimeError, match="num_splits"):
+        _hip.decode(q, kc, vc, bt, cl, scale, num_splits=2, shared_pages=True)
