@@ -191,9 +191,12 @@ __device__ inline void gqa_wave_run(const RowAttnArgs& a, GqaWaveLds<D>& w, int 
 #pragma unroll
     for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[r]);
     mx = max_halves(mx);
-    if (__builtin_amdgcn_ballot_w64(mx > m + kSlack) != 0) {
-      const float m_new = fmaxf(m, mx);
-      const float corr = fast_exp2(m - m_new);
+    // Each slot decides for itself (the wave only skips the rescale when no
+    // slot needs it): a slot's result never depends on the other slots of its
+    // wave, whichever sequences or heads share it.
+    const float m_new = mx > m + kSlack ? mx : m;
+    if (__builtin_amdgcn_ballot_w64(m_new != m) != 0) {
+      const float corr = fast_exp2(m - m_new);   // 1 for slots that keep m
       l *= corr;
 #pragma unroll
       for (int d = 0; d < kDB; ++d)
@@ -330,118 +333,153 @@ void launch_typed(const RowAttnArgs& a, hipStream_t stream) {
 constexpr int kShareMaxB = 2048;   // sequences the plan kernel can group
 constexpr int kShareMin = 4;       // sequences that must hold a partition to group it
 
-constexpr int kShareMaxPages = 64; // pages of a partition (1024 tokens)
+constexpr int kShareMaxPages = 64; // pages of a partition (1024 tokens): one per lane
 
-// The n (>= 1) block ids from entry `first` of a table row of MB entries,
-// all loads issued at once and unconditionally (a load under a condition
-// makes the compiler wait for every earlier one): entries past n repeat id
-// n - 1, and indices are clamped to the row.
-__device__ inline void load_ids(const int32_t* row, int first, int n, int MB,
-                                int32_t (&v)[kShareMaxPages]) {
-#pragma unroll
-  for (int i = 0; i < kShareMaxPages; ++i) v[i] = row[min(first + min(i, n - 1), MB - 1)];
+// splitmix64 finaliser: a well-mixed 64-bit image of one (position, id).
+__device__ inline uint64_t mix64(uint64_t x) {
+  x ^= x >> 30;
+  x *= 0xbf58476d1ce4e5b9ull;
+  x ^= x >> 27;
+  x *= 0x94d049bb133111ebull;
+  return x ^ (x >> 31);
 }
 
-// 64-bit FNV-1a over the ids (equal hashes are then compared id by id, so a
-// collision only costs a comparison).
-__device__ inline uint64_t ids_hash(const int32_t (&v)[kShareMaxPages], int n) {
-  uint64_t h = 1469598103934665603ull;
-#pragma unroll
-  for (int i = 0; i < kShareMaxPages; ++i)
-    if (i < n) h = (h ^ (uint32_t)v[i]) * 1099511628211ull;
-  return h;
-}
+constexpr int kShareSlots = 2 * kShareMaxB;   // hash-table slots (a power of two)
 
-// One workgroup per partition index p.  A sequence's partition p is a
-// candidate when it is full (all part_tokens keys below its context).  Its
-// representative is the first sequence with the same hash, confirmed id by
-// id (a hash collision leaves the sequence on its own).  Groups of at least
-// kShareMin sequences are laid out in members[] in sequence order and cut
-// into units of per_unit sequences.  Every scan over the batch is a
-// branch-free sum or minimum, so its LDS reads pipeline.
-__global__ __launch_bounds__(256) void share_plan_kernel(RowAttnArgs a, SharePlanArgs s) {
+constexpr int kPlanWaves = 16;      // waves of a plan workgroup
+constexpr int kPlanBatch = 8;       // sequences whose loads a wave issues together
+
+// One workgroup per partition index p.  Its waves take batches of
+// kPlanBatch sequences, all of a batch's loads in flight together, the 64
+// lanes reading one sequence's block ids of the partition at once (up to 64
+// pages, one coalesced load).  A sequence's partition p is a candidate when
+// it is full (all part_tokens keys below its context); its hash is the
+// wave's sum of mix64(position, id).  The representative is the first
+// sequence with the same hash, found through an open-addressing table in LDS
+// and confirmed id by id (a hash collision leaves the sequence on its own).
+// Groups of at least kShareMin sequences get a range of members[] and of
+// units by atomic allocation, so the order of groups, and of sequences inside
+// a group, may differ between calls; no result depends on it (every query
+// slot of the matrix-core wave is computed on its own, its running max
+// included).
+__global__ __launch_bounds__(kPlanWaves * 64) void share_plan_kernel(RowAttnArgs a,
+                                                                     SharePlanArgs s) {
+  constexpr int kThreads = kPlanWaves * 64;
+  __shared__ uint64_t key[kShareSlots];       // hash of the slot's partition (~0: empty)
+  __shared__ int first[kShareSlots];          // lowest sequence with that hash
   __shared__ uint64_t hsh[kShareMaxB];
   __shared__ int rep[kShareMaxB];
-  __shared__ int cnt[kShareMaxB];
-  __shared__ int grp[kShareMaxB];    // members of the group b represents (0: none)
-  __shared__ int nun[kShareMaxB];    // units of that group
-  __shared__ int units_sum;
+  __shared__ int cnt[kShareMaxB];             // sequences per representative
+  __shared__ int moff[kShareMaxB];            // representative: its members[] offset
+  __shared__ int uoff[kShareMaxB];            // representative: its first unit
+  __shared__ int fill[kShareMaxB];            // representative: members placed so far
+  __shared__ int members_used, units_used;
   const int p = blockIdx.x;
   const int tid = threadIdx.x;
-  const int pages = a.part_tokens / 16;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int pages = a.part_tokens / 16;       // <= 64: one per lane
   const int64_t cap = (int64_t)a.MB * a.BS;
-  if (tid == 0) units_sum = 0;
-  for (int b = tid; b < a.B; b += 256) {
-    const int64_t end = a.ctx[b] < cap ? a.ctx[b] : cap;
-    const bool full = (int64_t)(p + 1) * a.part_tokens <= end;
-    int32_t v[kShareMaxPages];
-    load_ids(a.bt + (int64_t)b * a.MB, p * pages, pages, a.MB, v);
-    hsh[b] = full ? ids_hash(v, pages) : ~0ull;
+  const int col = min(p * pages + min(lane, pages - 1), a.MB - 1);   // this lane's table entry
+  for (int i = tid; i < kShareSlots; i += kThreads) {
+    key[i] = ~0ull;
+    first[i] = 0x7fffffff;
+  }
+  for (int b = tid; b < a.B; b += kThreads) {
     cnt[b] = 0;
+    fill[b] = 0;
+  }
+  if (tid == 0) {
+    members_used = 0;
+    units_used = 0;
   }
   __syncthreads();
-  for (int b = tid; b < a.B; b += 256) {
-    int r = -1;
-    const uint64_t hb = hsh[b];
-    if (hb != ~0ull) {
-      r = b;
-#pragma unroll 8
-      for (int c = 0; c < b; ++c) r = (hsh[c] == hb && c < r) ? c : r;
-      if (r != b) {
-        int32_t mine[kShareMaxPages], other[kShareMaxPages];
-        load_ids(a.bt + (int64_t)b * a.MB, p * pages, pages, a.MB, mine);
-        load_ids(a.bt + (int64_t)r * a.MB, p * pages, pages, a.MB, other);
-        bool same = true;
+  for (int b0 = wave * kPlanBatch; b0 < a.B; b0 += kPlanWaves * kPlanBatch) {
+    int id[kPlanBatch], ctx[kPlanBatch];
 #pragma unroll
-        for (int i = 0; i < kShareMaxPages; ++i) same = same && mine[i] == other[i];
-        if (!same) r = b;
+    for (int k = 0; k < kPlanBatch; ++k) {
+      const int b = min(b0 + k, a.B - 1);
+      id[k] = a.bt[(int64_t)b * a.MB + col];
+      ctx[k] = a.ctx[b];
+    }
+#pragma unroll
+    for (int k = 0; k < kPlanBatch; ++k) {
+      const int b = b0 + k;
+      if (b >= a.B) break;                     // wave-uniform
+      const int64_t end = ctx[k] < cap ? ctx[k] : cap;
+      const bool full = (int64_t)(p + 1) * a.part_tokens <= end;
+      uint64_t h = lane < pages ? mix64(((uint64_t)lane << 32) | (uint32_t)id[k]) : 0;
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) h += __shfl_xor(h, off);
+      if (!full || h == ~0ull) h = ~0ull;
+      if (lane == 0) {
+        hsh[b] = h;
+        if (h != ~0ull) {
+          // insert: claim an empty slot or find this hash's, then lower its index
+          for (int i = (int)(h & (kShareSlots - 1));; i = (i + 1) & (kShareSlots - 1)) {
+            const uint64_t old = atomicCAS(&key[i], ~0ull, h);
+            if (old == ~0ull || old == h) {
+              atomicMin(&first[i], b);
+              break;
+            }
+          }
+        }
       }
     }
-    rep[b] = r;
   }
   __syncthreads();
-  // a collision can leave a sequence whose representative kept another
-  // representative: only sequences whose representative represents itself
-  // are counted
-  for (int b = tid; b < a.B; b += 256) {
+  for (int b0 = wave * kPlanBatch; b0 < a.B; b0 += kPlanWaves * kPlanBatch) {
+    int r[kPlanBatch], mine[kPlanBatch], other[kPlanBatch];
+#pragma unroll
+    for (int k = 0; k < kPlanBatch; ++k) {
+      const int b = min(b0 + k, a.B - 1);
+      const uint64_t h = hsh[b];
+      r[k] = -1;
+      if (h != ~0ull) {
+        int i = (int)(h & (kShareSlots - 1));
+        while (key[i] != h) i = (i + 1) & (kShareSlots - 1);
+        r[k] = first[i];
+      }
+      mine[k] = a.bt[(int64_t)b * a.MB + col];
+      other[k] = a.bt[(int64_t)max(r[k], 0) * a.MB + col];
+    }
+#pragma unroll
+    for (int k = 0; k < kPlanBatch; ++k) {
+      const int b = b0 + k;
+      if (b >= a.B) break;                     // wave-uniform
+      int rk = r[k];
+      if (rk >= 0 && rk != b && __builtin_amdgcn_ballot_w64(mine[k] != other[k]) != 0) rk = b;
+      if (lane == 0) rep[b] = rk;
+    }
+  }
+  __syncthreads();
+  // a sequence that fell back to itself after a collision is not counted
+  // with the group of the hash's first sequence
+  for (int b = tid; b < a.B; b += kThreads) {
     const int r = rep[b];
     if (r >= 0 && rep[r] == r) atomicAdd(&cnt[r], 1);
   }
   __syncthreads();
-  int my_units = 0;
-  for (int b = tid; b < a.B; b += 256) {
-    const bool g = rep[b] == b && cnt[b] >= kShareMin;
-    grp[b] = g ? cnt[b] : 0;
-    nun[b] = g ? (cnt[b] + s.per_unit - 1) / s.per_unit : 0;
-    my_units += nun[b];
+  for (int r = tid; r < a.B; r += kThreads) {
+    if (rep[r] != r || cnt[r] < kShareMin) continue;
+    const int n = cnt[r];
+    const int nu = (n + s.per_unit - 1) / s.per_unit;
+    const int off = atomicAdd(&members_used, n);
+    const int u0 = atomicAdd(&units_used, nu);
+    moff[r] = off;
+    uoff[r] = u0;
+    for (int k = 0; k < nu; ++k)
+      s.units[(int64_t)p * s.U + u0 + k] =
+          make_int4(off + k * s.per_unit, min(s.per_unit, n - k * s.per_unit), r, 0);
   }
   __syncthreads();
-  for (int b = tid; b < a.B; b += 256) {
+  for (int b = tid; b < a.B; b += kThreads) {
     const int r = rep[b];
-    const bool grouped = r >= 0 && grp[r] > 0;
+    const bool grouped = r >= 0 && rep[r] == r && cnt[r] >= kShareMin;
     s.skip[(int64_t)b * a.P + p] = grouped ? 1 : 0;
-    if (!grouped) continue;
-    // members[] offset and unit offset of the group: sums over the groups of
-    // lower representatives; index of b inside its group
-    int off = 0, uoff = 0, idx = 0;
-#pragma unroll 8
-    for (int c = 0; c < r; ++c) {
-      off += grp[c];
-      uoff += nun[c];
-    }
-#pragma unroll 8
-    for (int c = r; c < b; ++c) idx += rep[c] == r;
-    s.members[(int64_t)p * a.B + off + idx] = b;
-    if (b == r) {
-      const int n = grp[r];
-      for (int k = 0; k < nun[r]; ++k)
-        s.units[(int64_t)p * s.U + uoff + k] =
-            make_int4(off + k * s.per_unit, min(s.per_unit, n - k * s.per_unit), r, 0);
-    }
+    if (grouped) s.members[(int64_t)p * a.B + moff[r] + atomicAdd(&fill[r], 1)] = b;
   }
-  if (my_units) atomicAdd(&units_sum, my_units);
-  __syncthreads();
-  if (tid == 0) s.n_units[p] = units_sum;
+  if (tid == 0) s.n_units[p] = units_used;
 }
 
 constexpr int kShareGroups = 256;   // workgroups of the shared-page grid
@@ -572,7 +610,8 @@ int share_unit_slots(int B, int per_unit) {
 }
 
 void launch_share_plan(const RowAttnArgs& a, const SharePlanArgs& s, hipStream_t stream) {
-  hipLaunchKernelGGL(share_plan_kernel, dim3((unsigned)a.P), dim3(256), 0, stream, a, s);
+  hipLaunchKernelGGL(share_plan_kernel, dim3((unsigned)a.P), dim3(kPlanWaves * 64), 0, stream,
+                     a, s);
 }
 
 void launch_shared_pages(const RowAttnArgs& a, const SharePlanArgs& s, int kv_dtype, int D,

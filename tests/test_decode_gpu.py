@@ -442,6 +442,15 @@ def test_shared_pages_decode(H, Hkv, D, dtype, pt, ctx, groups):
     for b in range(len(ctx)):
         if b not in grouped:
             assert torch.equal(shared[b], plain[b]), b
+    # a sequence's result depends on nothing but its own query and pages: the
+    # same call again, and the batch in reverse order, give the same bits
+    again = _hip.decode(q, kc, vc, bt, cl, scale, num_splits=0, partition_tokens=pt,
+                        shared_pages=True)
+    assert torch.equal(again, shared)
+    flip = torch.arange(len(ctx) - 1, -1, -1, device=DEV)
+    rev = _hip.decode(q[flip].contiguous(), kc, vc, bt[flip].contiguous(), cl[flip].contiguous(),
+                      scale, num_splits=0, partition_tokens=pt, shared_pages=True)
+    assert torch.equal(rev[flip], shared)
 
 
 def test_shared_pages_c5():
