@@ -420,6 +420,11 @@ def _oracle_rows(q, kc, vc, bt, ctx, scale, rows):
      [(range(0, 40), 128)]),
     # 70 sharers of 256-token partitions: units of 32, 32 and 6
     (4, 4, 32, torch.bfloat16, 256, [1300 + 11 * i for i in range(70)], [(range(0, 70), 80)]),
+    # 8 and 16 query heads per KV head: the unshared partitions run on the
+    # matrix-core GQA kernel, which skips the shared ones too
+    (32, 4, 128, torch.bfloat16, 0, [1100 + 57 * i for i in range(12)] + [300, 5000],
+     [(range(0, 12), 64)]),
+    (32, 2, 64, torch.float16, 0, [700 + 90 * i for i in range(9)], [(range(0, 9), 40)]),
 ])
 def test_shared_pages_decode(H, Hkv, D, dtype, pt, ctx, groups):
     """Sequences holding the same pages: their shared partitions are read once
