@@ -484,6 +484,7 @@ void prefill_mfma_kernel(PrefillArgs a) {
                           ? 0
                           : min(kNKB, (w_lim_max - tile_key0) / 32 + 1);
 
+      half8 kn[kDC16];   // K fragments of the next block of this tile
   #pragma unroll
       for (int kb = 0; kb < kNKB; ++kb) {
         // Producer share of this block: V at block 0, K chunks spread over the
@@ -503,7 +504,17 @@ void prefill_mfma_kernel(PrefillArgs a) {
         }
         if (kb >= nkb) continue;
 
-        float16x s = qk_block<D>(t, kb, qf, j, hh);
+        // S^T of block 0 reads its K fragments here; those of block 1 were read
+        // during block 0's softmax (measured +2% on C4, bit-identical)
+        float16x s;
+        if (kb == 0) {
+          s = qk_block<D>(t, kb, qf, j, hh);
+        } else {
+  #pragma unroll
+          for (int r = 0; r < 16; ++r) s[r] = 0.0f;
+  #pragma unroll
+          for (int c = 0; c < kDC16; ++c) s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kn[c], qf[c], s, 0, 0, 0);
+        }
 
         // V^T fragments of this block, read before the softmax so that their
         // latency hides behind it.
@@ -514,6 +525,11 @@ void prefill_mfma_kernel(PrefillArgs a) {
           for (int d = 0; d < kDB; ++d)
             vf[kc][d] =
                 *reinterpret_cast<const half8*>(&t.vt[d * 32 + j][kb * 32 + kc * 16 + 8 * hh]);
+        if (kb + 1 < kNKB) {
+  #pragma unroll
+          for (int c = 0; c < kDC16; ++c)
+            kn[c] = *reinterpret_cast<const half8*>(&t.k[(kb + 1) * 32 + j][16 * c + 8 * hh]);
+        }
 
         // mask: accumulator register r of half hh holds key key0 + 16*(r/8) + 8*hh + r%8
         const int key0 = tile_key0 + kb * 32;
