@@ -410,6 +410,75 @@ def cpu_baseline(case, n_seq: int = 0, seed: int = 7) -> dict:
     }
 
 
+def cpu_prefill_baseline(case, heads: int = 0) -> dict:
+    """The prefill oracle (oracle/attention.py prefill_one, the reference's
+    paged_attention_prefill_torch per sequence) over every sequence of the
+    case for `heads` of its heads (all of them when 0); useful causal FLOPs of
+    that sample over the summed median times."""
+    import torch
+
+    from oracle.attention import prefill_one
+
+    threads = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    D = case.head_dim
+    heads = heads or case.n_heads
+    cu = case.cu_seqlens.cpu().tolist()
+    total, flops = 0.0, 0
+    for b in range(len(case.ctx)):
+        n, S = int(case.ctx[b]), cu[b + 1] - cu[b]
+        nblk = -(-n // 16)
+        blocks = case.block_tables[b, :nblk].long()
+        q = case.q[cu[b]:cu[b + 1], :heads].cpu()
+        kb = case.k_cache.index_select(0, blocks)[:, :, :heads].cpu()
+        vb = case.v_cache.index_select(0, blocks)[:, :, :heads].cpu()
+        tbl = torch.arange(nblk, dtype=torch.int32)
+        prefill_one(q, kb, vb, tbl, n, case.scale)           # warm-up
+        runs = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            prefill_one(q, kb, vb, tbl, n, case.scale)
+            runs.append(time.perf_counter() - t0)
+        total += statistics.median(runs)
+        P = n - S
+        flops += 4 * heads * D * (S * P + S * (S + 1) // 2)
+    return {
+        "value": round(flops / total / 1e12, 4), "unit": "TFLOP/s",
+        "cores": torch.get_num_threads(), "kind": "port",
+        "sample": (f"all {len(case.ctx)} {case.name} sequences, {heads} of {case.n_heads} heads, "
+                   f"oracle/attention.py prefill_one (torch fp32 CPU), median of 3 after 1 "
+                   f"warm-up, summed: {total * 1e3:.1f} ms for {flops / 1e9:.2f} useful GFLOP"),
+    }
+
+
+def cpu_pack_baseline(n: int = 1024, pool_blocks: int = 2048, seed: int = 43) -> dict:
+    """The pack oracle (oracle/kvpack.py export_blocks, the reference's
+    pool[:, :, idx].permute(2, 0, 1, ...).contiguous() in numpy) gathering n
+    random blocks of C5's page shape from a host pool; read + write bytes."""
+    import numpy as np
+
+    from oracle.kvpack import export_blocks
+
+    rng = np.random.default_rng(seed)
+    pool = rng.integers(0, 1 << 16, size=(1, 2, pool_blocks, 16, 32, 128), dtype=np.uint16)
+    ids = rng.choice(pool_blocks, size=n, replace=False).tolist()
+    export_blocks(pool, ids)                                 # warm-up
+    runs = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        out = export_blocks(pool, ids)
+        runs.append(time.perf_counter() - t0)
+    t = statistics.median(runs)
+    nbytes = 2 * out.nbytes
+    return {
+        "value": round(nbytes / t / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+        "sample": (f"{n} random blocks of [1, 2, 16, 32, 128] 16-bit elements from a "
+                   f"{pool_blocks}-block host pool, oracle/kvpack.py export_blocks (numpy), "
+                   f"median of 3 after 1 warm-up: {t * 1e3:.1f} ms for {nbytes / 1e6:.0f} MB "
+                   f"read + written"),
+    }
+
+
 # ---------------------------------------------------------------------------
 
 
@@ -483,6 +552,10 @@ def main() -> int:
                 "useful_flops": pre["flops"],
             }
             log(f"C4 prefill: {pre['step_ms'] * 1e3:.1f} us, {pre['kernel_tflops']:.1f} TFLOP/s")
+            if not args.no_cpu:
+                secondary["C4_prefill"]["cpu_baseline"] = cpu_prefill_baseline(pc)
+                log(f"C4 prefill cpu baseline: "
+                    f"{secondary['C4_prefill']['cpu_baseline']['value']} TFLOP/s")
             del pc
         except RuntimeError as exc:
             secondary["C4_prefill"] = {"error": str(exc)[:200]}
@@ -495,6 +568,9 @@ def main() -> int:
         }
         log(f"C5 pack: {pk['kernel_ms'] * 1e3:.1f} us, {pk['kernel_gbs']:.0f} GB/s, "
             f"exact={pk['bit_exact']}")
+        if not args.no_cpu:
+            secondary["C5_pack"]["cpu_baseline"] = cpu_pack_baseline()
+            log(f"C5 pack cpu baseline: {secondary['C5_pack']['cpu_baseline']['value']} GB/s")
         kw = kv_write_leg(max(20, args.steps // 5), 10)
         secondary["C5_kv_write"] = {
             "us_per_step": round(kw["step_ms"] * 1e3, 2), "gbs": round(kw["kernel_gbs"], 1),
