@@ -529,7 +529,10 @@ def main() -> int:
         "head_dim": case.head_dim, "block_size": 16, "kv_dtype": kv_dtype,
         "sum_context": int(case.ctx.sum()), "max_context": int(case.ctx.max()),
         "num_blocks": int(case.k_cache.shape[0]),
-        "decomposition": f"fixed partitions of {args.partition or 512} tokens + LSE merge",
+        "decomposition": (f"fixed partitions of {args.partition} tokens + LSE merge"
+                          if args.partition else
+                          "library default partitions (512 tokens, halved down to 32 while "
+                          "the grid has fewer than 4 waves per CU) + LSE merge"),
         "parallelism": "none (one GPU)",
     }
     if case.meta.get("shared_blocks"):

@@ -238,6 +238,31 @@ def test_split_invariance_and_partition_sizes():
         assert _maxerr(o, outs[0]) <= 1e-4
 
 
+def test_small_grid_default_partition():
+    """With the library's default decomposition a small batch gets shorter
+    partitions (more waves on the CUs): C1's 8 x 12 rows with a 512-token
+    table run 32-token partitions (16 per row, the workspace says so), and the
+    result agrees with explicit 512-token partitions and the oracle."""
+    from heteroserve import _hip
+
+    _mods()
+    lib = _hip.lib()
+    B, H, D, MB = 8, 12, 64, 32
+    ws = lib.hs_decode_workspace_bytes(B, H, H, D, 16, MB, 0, 0)
+    acc = B * H * 16 * D * 4
+    assert ws == (acc + 255) // 256 * 256 + B * H * 16 * 2 * 4
+    big = lib.hs_decode_workspace_bytes(64, 32, 32, 128, 16, 512, 0, 0)
+    assert big == 64 * 32 * 16 * 128 * 4 + 64 * 32 * 16 * 2 * 4   # C2 keeps 512 tokens
+    pool, q, bt, ctx = _random_case([16, 100, 257, 300, 401, 480, 511, 512], H, H, D, 16,
+                                    torch.float16, seed=33)
+    kp, vp = pool[0, 0], pool[0, 1]
+    scale = D ** -0.5
+    got = _hip.decode(q, kp, vp, bt, ctx, scale, 0)
+    fixed = _hip.decode(q, kp, vp, bt, ctx, scale, 0, partition_tokens=512)
+    assert _maxerr(got, _oracle(q, kp, vp, bt, ctx, scale)) <= 2e-3
+    assert _maxerr(got, fixed) <= 1e-4
+
+
 @pytest.mark.parametrize("H,Hkv,D,dtype", [
     (32, 8, 128, torch.bfloat16),   # llama3-8b shape (config.py:85-93), G = 4
     (32, 1, 128, torch.bfloat16),   # MQA: one wave serves all 32 query heads
