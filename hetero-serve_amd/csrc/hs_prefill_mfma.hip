@@ -381,7 +381,9 @@ void prefill_mfma_kernel(PrefillArgs a) {
   // workgroups of one part stream the same K/V at the same time; the longest
   // tile's parts set the span either way.
   const int kt_all = kend > 0 ? (kend + kBN - 1) / kBN : 0;
-  const int kt_seq = (min(cap, ctx_b) + kBN - 1) / kBN;
+  // (a negative context, invalid input, counts as empty: kt0 and the table
+  // offset below stay >= 0)
+  const int kt_seq = (max(0, min(cap, ctx_b)) + kBN - 1) / kBN;
   const int per_part = (kt_seq + a.n_split - 1) / a.n_split;
   const int kt0 = min(kt_all, part * per_part);
   const int kt1 = min(kt_all, kt0 + per_part);

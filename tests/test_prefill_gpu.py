@@ -182,6 +182,33 @@ def test_varlen_matches_per_sequence_calls():
             assert _maxerr(got[cu[b]:cu[b + 1]], want) <= 2e-3, (mfma, b)
 
 
+def test_negative_context_is_empty():
+    """A negative context length (invalid input; the values live on the device,
+    so the host cannot reject them) gives that sequence zero rows and leaves
+    its neighbours exact, through the key-range split (a small grid) as well
+    as the unsplit launch."""
+    from heteroserve import _hip
+
+    _wmma()
+    from hsbench.cases import build_prefill
+
+    case = build_prefill("t", np.array([100, 300, 0]), np.array([40, 129, 64]),
+                         8, 8, 128, 200, torch.bfloat16, DEV, seed=9)
+    ctx = case.context_lens.clone()
+    ctx[0] = -1000
+    cu = case.cu_seqlens.cpu().numpy()
+    for split in (True, False):
+        got = _hip.prefill_varlen(case.q, case.cu_seqlens, int(case.q_lens.max()), case.k_cache,
+                                  case.v_cache, case.block_tables, ctx, case.scale,
+                                  use_mfma=True, split=split)
+        assert torch.all(got[cu[0]:cu[1]] == 0), split
+        for b in (1, 2):
+            want = prefill_one(case.q[cu[b]:cu[b + 1]].cpu(), case.k_cache.cpu(),
+                               case.v_cache.cpu(), case.block_tables[b].cpu(), int(case.ctx[b]),
+                               case.scale)
+            assert _maxerr(got[cu[b]:cu[b + 1]], want) <= 2e-3, (split, b)
+
+
 @pytest.mark.parametrize("name", ["C4", "C5-prefill"])
 def test_prefill_configs(name):
     """Full-size chunked prefill through the MFMA kernel: every sequence's
