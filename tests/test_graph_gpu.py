@@ -1,0 +1,80 @@
+"""The attention and pack calls under HIP graph capture.
+
+Serving loops capture their decode step to cut launch overhead.  Nothing on
+these paths allocates with hipMalloc, fills memory or synchronises with the
+host, so the calls capture as they are (outputs and workspaces come from
+torch's allocator, which serves a capture from the graph's pool).  Each graph
+is replayed several times, with eager work and synchronisations between the
+replays, and every replay must equal the eager result bit for bit.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def _capture(fn):
+    """Warm up on a side stream (default priority), then capture fn()."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = fn()
+    return graph, out
+
+
+def _replays_match(graph, outs, wants, n=3):
+    for i in range(n):
+        for o in outs:
+            o.fill_(float("nan") if o.is_floating_point() else -1)   # eager work between
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for o, w in zip(outs, wants):
+            assert torch.equal(o, w), f"replay {i}"
+
+
+def test_decode_prefill_and_pack_replay_bit_exact():
+    from heteroserve import _hip
+    from heteroserve.model import paged_attn, paged_attn_wmma
+    from hsbench.cases import build_decode, build_prefill
+
+    assert _hip.ready(), _hip.error()
+    dec = build_decode("g", np.array([1, 300, 1100, 4000, 17]), 8, 8, 128, 800,
+                       torch.bfloat16, DEV, seed=12)
+    dec_args = (dec.q, dec.k_cache, dec.v_cache, dec.block_tables, dec.context_lens, dec.scale)
+    # a single chunk: a small grid, so the MFMA prefill splits the key range
+    # and runs its merge kernel too
+    pre = build_prefill("g", np.array([700]), np.array([300]), 8, 8, 128, 80,
+                        torch.bfloat16, DEV, seed=13)
+    q4 = pre.q.unsqueeze(0)
+    pre_args = (q4, pre.k_cache, pre.v_cache, pre.block_tables, pre.context_lens, pre.scale)
+    pool = dec.pool
+    ids = torch.tensor([5, 0, 799, 42, 42, 7], dtype=torch.int64, device=DEV)
+    packed = torch.empty((ids.numel(),) + tuple(pool.shape[:2]) + tuple(pool.shape[3:]),
+                         dtype=pool.dtype, device=DEV)
+
+    want_dec = paged_attn.paged_attention(*dec_args)
+    want_pre = paged_attn_wmma.paged_attention_prefill_wmma(*pre_args)
+    _hip.kv_pack(pool, ids, packed)
+    want_pack = packed.clone()
+    torch.cuda.synchronize()
+
+    def step():
+        d = paged_attn.paged_attention(*dec_args)
+        p = paged_attn_wmma.paged_attention_prefill_wmma(*pre_args)
+        _hip.kv_pack(pool, ids, packed)
+        return d, p
+
+    graph, (d, p) = _capture(step)
+    _replays_match(graph, [d, p, packed], [want_dec, want_pre, want_pack])
