@@ -8,13 +8,8 @@
 // (m, l, acc) are combined by a log-sum-exp merge.  The softmax runs in base 2
 // with scale * log2(e) folded into q, so every exponential is one v_exp_f32.
 //
-// Wave layout (gfx950, wave64).  A 16-byte load holds kVec KV elements, so one
-// token's head row of D elements is spread over kLpt = D / kVec lanes, and one
-// wave-wide load instruction covers kTpl = 64 / kLpt tokens.  For bf16 at
-// D = 128 that is 16 lanes per token and 4 tokens per load: a token's dot
-// product is reduced inside one 16-lane DPP row, with no LDS traffic.  Each
-// group of kLpt lanes ("slot") runs its own online softmax over the tokens it
-// loads; the kTpl slot states are merged once at the end of the partition.
+// The walk of one wave (16-lane token slots, DPP reductions, per-slot softmax
+// states merged at the end) is RowWalk, hs_rowwalk.h.
 // A workgroup is kDecodeWaves waves = consecutive heads (or GQA head groups)
 // of the same (row, partition), and the head group is the fastest-varying grid
 // index, so the
@@ -26,11 +21,11 @@
 // 5.8 TB/s, 32 tokens of loads in flight per wave and 512-token partitions
 // to ~6 TB/s.
 #include "hs_kernels.h"
+#include "hs_rowwalk.h"
 
 namespace hs {
 
 constexpr int kDecodeWaves = 2;  // waves per workgroup
-constexpr float kDecodeSlack = 8.0f;  // lazy raise of the running max, log2 units
 
 // One wave = G query heads of one KV group for one (row, partition): each
 // 16-byte K/V load feeds G dot products, so a GQA group's pages are read once
@@ -38,15 +33,8 @@ constexpr float kDecodeSlack = 8.0f;  // lazy raise of the running max, log2 uni
 // arithmetic of each head is the same for every G (same slots, token order
 // and reduction order), so packing does not change results.
 template <typename T, int D, bool kPaged, int G>
-__global__ __launch_bounds__(kDecodeWaves * 64) void row_attn_part_kernel(RowAttnArgs a) {
-  constexpr int kVec = Elem<T>::kVec;
-  constexpr int kLpt = D / kVec;           // lanes per token
-  constexpr int kTpl = 64 / kLpt;          // tokens per wave-wide load
-  constexpr int kU0 = kTpl >= 32 ? 1 : (32 / kTpl < 8 ? 32 / kTpl : 8);
-  constexpr int kU = kU0 / G > 1 ? kU0 / G : 1;   // loads in flight (registers shrink with G)
-  constexpr int kStep = kTpl * kU;         // tokens per loop iteration
-  static_assert(kLpt >= 1 && kLpt <= 64 && 64 % kLpt == 0, "head_dim / lane split");
-
+__global__ __launch_bounds__(kDecodeWaves * 64)
+__attribute__((amdgpu_waves_per_eu(G >= 8 ? 2 : (D > 128 ? 3 : 4)))) void row_attn_part_kernel(RowAttnArgs a) {
   const int lane = threadIdx.x & 63;
   const int n_hw = a.H / G;                                     // head groups of G
   const int n_groups = (n_hw + kDecodeWaves - 1) / kDecodeWaves;
@@ -71,150 +59,18 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void row_attn_part_kernel(RowAtt
     return;
   }
 
-  const int r = lane / kLpt;  // token slot
-  const int c = lane % kLpt;  // element chunk
-  const int kvh = h0 / (a.H / a.Hkv);
-  const int64_t tok_stride = (int64_t)a.Hkv * D;
-  const int64_t blk_stride = tok_stride * a.BS;
-  const T* kp = reinterpret_cast<const T*>(a.k) + kvh * D + c * kVec;
-  const T* vp = reinterpret_cast<const T*>(a.v) + kvh * D + c * kVec;
-  const int32_t* bt = a.bt + (int64_t)b * a.MB;
-
-  float qv[G][kVec];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const float4* q4 = reinterpret_cast<const float4*>(a.q + orow0 + g * D + c * kVec);
-#pragma unroll
-    for (int i = 0; i < kVec / 4; ++i) {
-      const float4 x = q4[i];
-      qv[g][4 * i + 0] = x.x * a.qscale;
-      qv[g][4 * i + 1] = x.y * a.qscale;
-      qv[g][4 * i + 2] = x.z * a.qscale;
-      qv[g][4 * i + 3] = x.w * a.qscale;
-    }
-  }
-
-  float m[G], l[G];
-  float acc[G][kVec];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    m[g] = kNegBig;
-    l[g] = 0.0f;
-#pragma unroll
-    for (int e = 0; e < kVec; ++e) acc[g][e] = 0.0f;
-  }
-
-  // Groups of kTpl tokens start at multiples of kTpl, so with kPaged
-  // (BS % kTpl == 0) a group never straddles a page and its block id is
-  // wave-uniform.  Addresses of groups past the range are clamped to the last
-  // group that holds a live token; their scores are masked below.
-  const int t_begin = lo - (lo % kTpl);
-  const int last_group = (hi - 1) - ((hi - 1) % kTpl);
-
-  for (int t0 = t_begin; t0 < hi; t0 += kStep) {
-    uint4 kr[kU], vr[kU];
-#pragma unroll
-    for (int u = 0; u < kU; ++u) {
-      const int tg = min(t0 + u * kTpl, last_group);
-      int64_t off;
-      if constexpr (kPaged) {
-        off = safe_block(bt[tg / a.BS], a.NB) * blk_stride +
-              (int64_t)(tg % a.BS + r) * tok_stride;
-      } else {
-        const int t = min(tg + r, hi - 1);
-        off = safe_block(bt[t / a.BS], a.NB) * blk_stride + (int64_t)(t % a.BS) * tok_stride;
-      }
-      kr[u] = load16_stream(kp + off);
-      vr[u] = load16_stream(vp + off);
-    }
-
-    bool ok[kU];
-#pragma unroll
-    for (int u = 0; u < kU; ++u) {
-      const int t = t0 + u * kTpl + r;
-      ok[u] = (t >= lo) && (t < hi);
-    }
-    float pu[G][kU];
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      float sc[kU];
-      float mx = kNegBig;
-#pragma unroll
-      for (int u = 0; u < kU; ++u) {
-        float kf[kVec];
-        Elem<T>::to_f32(kr[u], kf);
-        float d = 0.0f;
-#pragma unroll
-        for (int e = 0; e < kVec; ++e) d = fmaf(qv[g][e], kf[e], d);
-        d = group_sum<kLpt>(d);
-        sc[u] = ok[u] ? d : kNegBig;
-        mx = fmaxf(mx, sc[u]);
-      }
-      // The running max is raised only when this step's max exceeds it by
-      // more than kDecodeSlack (log2 units): probabilities stay <= 2^slack in
-      // fp32 and the G accumulators are rescaled on few steps.
-      if (__builtin_amdgcn_ballot_w64(mx > m[g] + kDecodeSlack) != 0) {
-        const float m_new = fmaxf(m[g], mx);
-        const float corr = fast_exp2(m[g] - m_new);
-        l[g] *= corr;
-#pragma unroll
-        for (int e = 0; e < kVec; ++e) acc[g][e] *= corr;
-        m[g] = m_new;
-      }
-      float psum = 0.0f;
-#pragma unroll
-      for (int u = 0; u < kU; ++u) {
-        pu[g][u] = ok[u] ? fast_exp2(sc[u] - m[g]) : 0.0f;
-        psum += pu[g][u];
-      }
-      l[g] += psum;
-    }
-#pragma unroll
-    for (int u = 0; u < kU; ++u) {
-      float vf[kVec];
-      Elem<T>::to_f32(vr[u], vf);
-#pragma unroll
-      for (int g = 0; g < G; ++g)
-#pragma unroll
-        for (int e = 0; e < kVec; ++e) acc[g][e] = fmaf(pu[g][u], vf[e], acc[g][e]);
-    }
-  }
-
-  // Merge the kTpl slot states: lanes with the same chunk c, different slot.
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-#pragma unroll
-    for (int off = kLpt; off < 64; off <<= 1) {
-      const float m_o = __shfl_xor(m[g], off);
-      const float l_o = __shfl_xor(l[g], off);
-      const float mm = fmaxf(m[g], m_o);
-      const float w_s = fast_exp2(m[g] - mm);
-      const float w_o = fast_exp2(m_o - mm);
-      l[g] = l[g] * w_s + l_o * w_o;
-#pragma unroll
-      for (int e = 0; e < kVec; ++e) acc[g][e] = acc[g][e] * w_s + __shfl_xor(acc[g][e], off) * w_o;
-      m[g] = mm;
-    }
-  }
-
-  if (r != 0) return;
+  RowWalk<T, D, kPaged, G> w;
+  w.run(KvPages{a.k, a.v, a.Hkv, a.BS, a.NB}, a.q + orow0, a.qscale, h0 / (a.H / a.Hkv),
+        a.bt + (int64_t)b * a.MB, lo, hi);
+  if (w.slot(lane) != 0) return;
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     const int h = h0 + g;
     if (nparts == 1) {
-      const float inv = l[g] > 0.0f ? 1.0f / l[g] : 0.0f;
-      float4* o4 = reinterpret_cast<float4*>(a.out + orow0 + g * D + c * kVec);
-#pragma unroll
-      for (int i = 0; i < kVec / 4; ++i)
-        o4[i] = make_float4(acc[g][4 * i] * inv, acc[g][4 * i + 1] * inv,
-                            acc[g][4 * i + 2] * inv, acc[g][4 * i + 3] * inv);
+      w.store_out(g, a.out + orow0 + g * D);
     } else {
       const int64_t pi = ((int64_t)row * a.H + h) * a.P + p;
-      float4* o4 = reinterpret_cast<float4*>(a.part_acc + pi * D + c * kVec);
-#pragma unroll
-      for (int i = 0; i < kVec / 4; ++i)
-        o4[i] = make_float4(acc[g][4 * i], acc[g][4 * i + 1], acc[g][4 * i + 2], acc[g][4 * i + 3]);
-      if (c == 0) *reinterpret_cast<float2*>(a.part_ml + 2 * pi) = make_float2(m[g], l[g]);
+      w.store_state(g, a.part_acc + pi * D, reinterpret_cast<float2*>(a.part_ml) + pi);
     }
   }
 }

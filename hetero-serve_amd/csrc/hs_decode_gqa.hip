@@ -45,6 +45,7 @@
 // while the current block is computed.
 #include "hs_kernels.h"
 #include "hs_mfma.h"
+#include "hs_rowwalk.h"
 
 namespace hs {
 
@@ -66,16 +67,29 @@ struct GqaWaveLds {
   _Float16 vt[D][kBlock + kVtPad];  // V of one block, transposed
 };
 
+// Adds x to a range-check sum; the empty asm pins the check next to the
+// conversion it checks (left free, the compiler sinks it into the next block
+// and keeps the converted words alive until then).
+__device__ inline void fold_check(float& chk, float x) {
+  chk += x;
+  asm volatile("" : "+v"(chk));
+}
+
 // One wave's partition pass: up to 32 query slots that read the same KV
 // head and the same pages, keys [lo, hi) of block table row `bt`.  Lane
 // (j, hh) serves slot j: its query starts at element q_off of a.q, and its
 // result goes either normalised to a.out at element out_off (`direct`, the
 // row's only partition) or as the partition state pi of a.part_acc /
 // a.part_ml.  Slots j >= gc are padding (zero query, nothing written).
+// Returns true (wave-uniform) when an fp16 operand of the pass was inf or
+// NaN: a scaled query of magnitude >= 65520 or, for a bf16 cache, a K/V value
+// >= 65536.  The state is then unusable and the caller recomputes the unit
+// in fp32.
 template <typename T, int D>
-__device__ inline void gqa_wave_run(const RowAttnArgs& a, GqaWaveLds<D>& w, int lane, int kvh,
+__device__ inline bool gqa_wave_run(const RowAttnArgs& a, GqaWaveLds<D>& w, int lane, int kvh,
                                     int gc, const int32_t* bt, int lo, int hi, int64_t q_off,
                                     float16x (&o)[D / 32], float& m, float& l) {
+  constexpr bool kCheckKv = std::is_same_v<T, Bf16>;
   constexpr int kDC16 = D / 16;     // QK k-steps
   constexpr int kDB = D / 32;       // 32-dim output blocks
   constexpr int kDC = D / 8;        // 16-byte chunks per head row
@@ -93,6 +107,7 @@ __device__ inline void gqa_wave_run(const RowAttnArgs& a, GqaWaveLds<D>& w, int 
 
   // Q^T fragments: lane (j, hh) holds slot j, dims 16c + 8hh .. +7.
   half8 qf[kDC16];
+  float chk = 0.0f;   // range check of the fp16 words this lane made
   {
     const float sc = j < gc ? a.qscale : 0.0f;
     const float* qp = a.q + q_off + 8 * hh;
@@ -100,9 +115,10 @@ __device__ inline void gqa_wave_run(const RowAttnArgs& a, GqaWaveLds<D>& w, int 
     for (int c = 0; c < kDC16; ++c) {
       const float4 x0 = *reinterpret_cast<const float4*>(qp + 16 * c);
       const float4 x1 = *reinterpret_cast<const float4*>(qp + 16 * c + 4);
-      qf[c] = __builtin_bit_cast(
-          half8, make_uint4(pack_f16(x0.x * sc, x0.y * sc), pack_f16(x0.z * sc, x0.w * sc),
-                            pack_f16(x1.x * sc, x1.y * sc), pack_f16(x1.z * sc, x1.w * sc)));
+      const uint4 qw = make_uint4(pack_f16(x0.x * sc, x0.y * sc), pack_f16(x0.z * sc, x0.w * sc),
+                                  pack_f16(x1.x * sc, x1.y * sc), pack_f16(x1.z * sc, x1.w * sc));
+      chk = f16_check(qw, chk);
+      qf[c] = __builtin_bit_cast(half8, qw);
     }
   }
   const int64_t tok = (int64_t)a.Hkv * D;           // elements between tokens of a page
@@ -140,23 +156,34 @@ __device__ inline void gqa_wave_run(const RowAttnArgs& a, GqaWaveLds<D>& w, int 
 #pragma unroll
     for (int u = 0; u < kLi; ++u) {
       const int t = kTpi * u + slot;
-      *reinterpret_cast<uint4*>(&w.k[swap_bits23(t)][8 * ck]) = to_f16x8<T>(kr[u]);
+      const uint4 h = to_f16x8<T>(kr[u]);
+      if constexpr (kCheckKv) fold_check(chk, f16_check(h, 0.0f));
+      *reinterpret_cast<uint4*>(&w.k[swap_bits23(t)][8 * ck]) = h;
     }
 #pragma unroll
-    for (int ph = 0; ph < 2; ++ph)
+    for (int ph = 0; ph < 2; ++ph) {
+      const uint4* x = vr + kG * ph;
+      uint4 h1;   // kG == 1: the lane's 8 dims of one token, converted at once
+      if constexpr (kG == 1) {
+        h1 = to_f16x8<T>(x[0]);
+        if constexpr (kCheckKv) fold_check(chk, f16_check(h1, 0.0f));
+      }
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         _Float16* dst = &w.vt[8 * ck + e][16 * ph + kG * slot];
-        const uint4* x = vr + kG * ph;
         if constexpr (kG == 4) {
-          *reinterpret_cast<uint2*>(dst) =
-              make_uint2(pack_col<T>(x[0], x[1], e), pack_col<T>(x[2], x[3], e));
+          const uint32_t w0 = pack_col<T>(x[0], x[1], e), w1 = pack_col<T>(x[2], x[3], e);
+          if constexpr (kCheckKv) fold_check(chk, f16_check(w0, w1, 0.0f));
+          *reinterpret_cast<uint2*>(dst) = make_uint2(w0, w1);
         } else if constexpr (kG == 2) {
-          *reinterpret_cast<uint32_t*>(dst) = pack_col<T>(x[0], x[1], e);
+          const uint32_t w0 = pack_col<T>(x[0], x[1], e);
+          if constexpr (kCheckKv) fold_check(chk, f16_check(w0, w0, 0.0f));
+          *reinterpret_cast<uint32_t*>(dst) = w0;
         } else {
-          *dst = (_Float16)elem_f32<T>(x[0], e);
+          *dst = __builtin_bit_cast(half8, h1)[e];
         }
       }
+    }
   };
 
 #pragma unroll
@@ -225,7 +252,37 @@ __device__ inline void gqa_wave_run(const RowAttnArgs& a, GqaWaveLds<D>& w, int 
         o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pk[kc], o[d], 0, 0, 0);
       }
   }
+  return __builtin_amdgcn_ballot_w64(f16_check_failed(chk)) != 0;
+}
 
+// fp32 recomputation of a wave's unit (RowWalk, the VALU decode arithmetic):
+// query heads h0 .. h0 + gc - 1 of KV head kvh for keys [lo, hi) of `row`,
+// written as the matrix-core pass would have (normalised output when the
+// partition is the row's only one, else partition states).  One head per
+// walk: a walk of eight would need more registers than the matrix-core pass
+// and lower the kernel's occupancy (measured: 101 -> 227 VGPRs at head dim 32).
+template <typename T, int D, int G>
+__device__ inline void walk_heads_fp32(const RowAttnArgs& a, int kvh, int h0, const int32_t* bt,
+                                       int lo, int hi, int row, int p, bool direct) {
+  RowWalk<T, D, true, G> w;   // 16-token pages: a load group never straddles one
+  const int64_t orow0 = ((int64_t)row * a.H + h0) * D;
+  w.run(KvPages{a.k, a.v, a.Hkv, a.BS, a.NB}, a.q + orow0, a.qscale, kvh, bt, lo, hi);
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    if (direct) {
+      w.store_out(g, a.out + orow0 + g * D);
+    } else {
+      const int64_t pi = ((int64_t)row * a.H + h0 + g) * a.P + p;
+      w.store_state(g, a.part_acc + pi * D, reinterpret_cast<float2*>(a.part_ml) + pi);
+    }
+  }
+}
+
+template <typename T, int D>
+__device__ inline void gqa_unit_fp32(const RowAttnArgs& a, int kvh, int h0, int gc,
+                                     const int32_t* bt, int lo, int hi, int row, int p,
+                                     bool direct) {
+  for (int g = 0; g < gc; ++g) walk_heads_fp32<T, D, 1>(a, kvh, h0 + g, bt, lo, hi, row, p, direct);
 }
 
 // Result of slot j of a wave: lane (j, hh) owns dims d*32 + 8g + 4hh + 0..3.
@@ -260,15 +317,6 @@ __device__ inline void gqa_wave_store(const RowAttnArgs& a, int lane, int gc,
   }
 }
 
-template <typename T, int D>
-__device__ inline void gqa_wave(const RowAttnArgs& a, GqaWaveLds<D>& w, int lane, int kvh, int gc,
-                                const int32_t* bt, int lo, int hi, int64_t q_off, bool direct,
-                                int64_t out_off, int64_t pi) {
-  float16x o[D / 32];
-  float m, l;
-  gqa_wave_run<T, D>(a, w, lane, kvh, gc, bt, lo, hi, q_off, o, m, l);
-  gqa_wave_store<D>(a, lane, gc, o, m, l, direct, out_off, pi);
-}
 
 template <typename T, int D>
 __global__ __launch_bounds__(kGqaWaves * 64) __attribute__((amdgpu_waves_per_eu(2)))
@@ -306,9 +354,16 @@ void gqa_mfma_part_kernel(RowAttnArgs a) {
     }
     return;
   }
-  gqa_wave<T, D>(a, lds[wv], lane, kvh, gc, a.bt + (int64_t)b * a.MB, lo, hi,
-                 orow0 + (int64_t)min(j, gc - 1) * D, nparts == 1, orow0 + (int64_t)j * D,
-                 ((int64_t)row * a.H + h0 + j) * a.P + p);
+  const int32_t* bt = a.bt + (int64_t)b * a.MB;
+  float16x o[D / 32];
+  float m, l;
+  if (gqa_wave_run<T, D>(a, lds[wv], lane, kvh, gc, bt, lo, hi,
+                         orow0 + (int64_t)min(j, gc - 1) * D, o, m, l)) {
+    gqa_unit_fp32<T, D>(a, kvh, h0, gc, bt, lo, hi, row, p, nparts == 1);
+    return;
+  }
+  gqa_wave_store<D>(a, lane, gc, o, m, l, nparts == 1, orow0 + (int64_t)j * D,
+                    ((int64_t)row * a.H + h0 + j) * a.P + p);
 }
 
 int64_t grid_size(const RowAttnArgs& a) {
@@ -499,6 +554,10 @@ void shared_pages_kernel(RowAttnArgs a, SharePlanArgs s) {
   constexpr int kState = 16 * kDB + 2;           // floats per lane: o, m, l
   static_assert(kState * 64 * sizeof(float) <= sizeof(GqaWaveLds<D>), "state exchange");
   __shared__ GqaWaveLds<D> lds[kGqaWaves];
+  // per wave: its pass hit an fp16 operand it cannot hold (two sets, by item
+  // parity, so that a wave's flag for the next item never overwrites one
+  // another wave may still be reading)
+  __shared__ int range_fail[2][kGqaWaves];
   const int lane = threadIdx.x & 63;
   const int wv = threadIdx.x >> 6;
   const int j = lane & 31;
@@ -532,17 +591,34 @@ void shared_pages_kernel(RowAttnArgs a, SharePlanArgs s) {
     t.row_h = (int64_t)t.mb * a.H + t.kvh * G + js % G;
     return t;
   };
-  for (int item = blockIdx.x; item < total * a.Hkv; item += gridDim.x) {   // workgroup-uniform
+  int parity = 0;
+  for (int item = blockIdx.x; item < total * a.Hkv; item += gridDim.x, parity ^= 1) {   // workgroup-uniform
     float16x o[kDB];
     float m, l;
     {
       const Slot t = slot_of(item);
       const int lo = t.p * a.part_tokens + wv * span;
       const int hi = wv == kGqaWaves - 1 ? (t.p + 1) * a.part_tokens : lo + span;
-      gqa_wave_run<T, D>(a, lds[wv], lane, t.kvh, t.gc, a.bt + (int64_t)t.un.z * a.MB, lo, hi,
-                         t.row_h * D, o, m, l);
+      const bool fail = gqa_wave_run<T, D>(a, lds[wv], lane, t.kvh, t.gc,
+                                           a.bt + (int64_t)t.un.z * a.MB, lo, hi, t.row_h * D, o,
+                                           m, l);
+      if (lane == 0) range_fail[parity][wv] = fail;
     }
     __syncthreads();   // every wave is done with its K/V tiles
+    bool fail = false;
+#pragma unroll
+    for (int w = 0; w < kGqaWaves; ++w) fail |= range_fail[parity][w] != 0;
+    if (fail) {
+      // An operand fp16 cannot hold: hand the group's (sequence, partition)
+      // pairs back to the partition kernel, which runs after this one and
+      // computes them like any other partition.
+      if (wv == 0) {
+        const Slot t = slot_of(item);
+        if (j < t.un.y && lane < 32)
+          s.skip[(int64_t)s.members[(int64_t)t.p * a.B + t.un.x + j] * a.P + t.p] = 0;
+      }
+      continue;
+    }
     float* xs = reinterpret_cast<float*>(&lds[wv]);
     if (wv > 0) {
 #pragma unroll

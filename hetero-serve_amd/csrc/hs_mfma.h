@@ -5,6 +5,8 @@
 
 #include "hs_common.h"
 
+#include <type_traits>
+
 namespace hs {
 namespace mfma {
 
@@ -21,6 +23,23 @@ __device__ inline uint32_t pack_f16(float a, float b) {
   const half2x h = __builtin_convertvector((float2x){a, b}, half2x);  // v_cvt_pk_f16_f32, RNE
   return __builtin_bit_cast(uint32_t, h);
 }
+
+// Range check of fp16 MFMA operands.  fp16 holds magnitudes up to 65504: a
+// bf16 cache value of magnitude >= 65536, or a scaled query >= 65520, rounds
+// to inf.  The kernels fold every operand word they convert into an fp32
+// v_dot2_f32_f16 sum: products of finite halves stay below 2^33, so the sum
+// is finite unless some half was inf or NaN.  One instruction per one or two
+// words (f16_check(w, w, acc) checks a single word).
+__device__ inline float f16_check(uint32_t x, uint32_t y, float acc) {
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(half2x, x), __builtin_bit_cast(half2x, y), acc,
+                                false);
+}
+
+__device__ inline float f16_check(const uint4& w, float acc) {
+  return f16_check(w.z, w.w, f16_check(w.x, w.y, acc));
+}
+
+__device__ inline bool f16_check_failed(float acc) { return !__builtin_isfinite(acc); }
 
 // Element e (0..7) of 8 packed 16-bit KV values, widened to fp32 (exact).
 template <typename T>

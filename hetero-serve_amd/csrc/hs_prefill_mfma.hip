@@ -50,6 +50,7 @@
 // through that XCD's L2.
 #include "hs_kernels.h"
 #include "hs_mfma.h"
+#include "hs_rowwalk.h"
 
 #include <algorithm>
 #include <type_traits>
@@ -149,6 +150,7 @@ struct Producer {
   };
 
   int vid[2];          // block id of this lane's V page for tiles of parity 0 / 1
+  float chk;           // range check of the fp16 words this thread wrote (bf16 caches)
 
   // per-thread constants
   uint32_t koff;       // byte offset of this lane's K chunk inside a page (+ head)
@@ -159,6 +161,7 @@ struct Producer {
 
   __device__ inline void init(const PrefillArgs& a, int wave, int kvh) {
     const int tid = threadIdx.x;
+    chk = 0.0f;
     tok = (int64_t)a.Hkv * D;
     const int t_k = tid / kDC;
     koff = (uint32_t)(((t_k % 16) * tok + kvh * D + (tid % kDC) * 8) * 2);
@@ -201,34 +204,45 @@ struct Producer {
   }
 
   // Registers -> LDS (fp16; K with the bit-2/3 row swap, V transposed).
+  // Only a bf16 cache can hold values fp16 cannot; those words are checked.
+  // The empty asm pins each check next to its conversion: left free, the
+  // compiler sinks the checks into the next tile and keeps the converted
+  // words alive until then (+14 VGPRs for K's, +16 for V's, measured).
+  __device__ inline void fold_check(float x) {
+    chk += x;
+    asm volatile("" : "+v"(chk));
+  }
   template <typename T>
-  __device__ inline void store_k_chunk(PrefillTileLds<D>& s, const Regs& r, int u) const {
+  __device__ inline void store_k_chunk(PrefillTileLds<D>& s, const Regs& r, int u) {
     const int t_k = threadIdx.x / kDC;
     const int row0 = (t_k & ~31) | swap_bits23(t_k & 31);
-    *reinterpret_cast<uint4*>(&s.k[row0 + u * kKeysPerU][(threadIdx.x % kDC) * 8]) =
-        to_f16x8<T>(r.k[u]);
+    const uint4 h = to_f16x8<T>(r.k[u]);
+    if constexpr (std::is_same_v<T, Bf16>) fold_check(f16_check(h, 0.0f));
+    *reinterpret_cast<uint4*>(&s.k[row0 + u * kKeysPerU][(threadIdx.x % kDC) * 8]) = h;
   }
 
   template <typename T>
-  __device__ inline void store_v(PrefillTileLds<D>& s, const Regs& r) const {
+  __device__ inline void store_v(PrefillTileLds<D>& s, const Regs& r) {
+    static_assert(kG == 2 || kG == 4, "V keys per thread");
     const int key0 = kG * (threadIdx.x % kGroups);
     const int dc = threadIdx.x / kGroups;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       _Float16* dst = &s.vt[dc * 8 + e][key0];
       if constexpr (kG == 4) {
-        *reinterpret_cast<uint2*>(dst) =
-            make_uint2(pack_col<T>(r.v[0], r.v[1], e), pack_col<T>(r.v[2], r.v[3], e));
-      } else if constexpr (kG == 2) {
-        *reinterpret_cast<uint32_t*>(dst) = pack_col<T>(r.v[0], r.v[1], e);
+        const uint32_t w0 = pack_col<T>(r.v[0], r.v[1], e), w1 = pack_col<T>(r.v[2], r.v[3], e);
+        if constexpr (std::is_same_v<T, Bf16>) fold_check(f16_check(w0, w1, 0.0f));
+        *reinterpret_cast<uint2*>(dst) = make_uint2(w0, w1);
       } else {
-        *dst = (_Float16)elem_f32<T>(r.v[0], e);
+        const uint32_t w0 = pack_col<T>(r.v[0], r.v[1], e);
+        if constexpr (std::is_same_v<T, Bf16>) fold_check(f16_check(w0, w0, 0.0f));
+        *reinterpret_cast<uint32_t*>(dst) = w0;
       }
     }
   }
 
   template <typename T>
-  __device__ inline void store_tile(PrefillTileLds<D>& s, const Regs& r) const {
+  __device__ inline void store_tile(PrefillTileLds<D>& s, const Regs& r) {
 #pragma unroll
     for (int u = 0; u < kKChunks; ++u) store_k_chunk<T>(s, r, u);
     store_v<T>(s, r);
@@ -322,6 +336,43 @@ __device__ inline bool ranked_tile(const PrefillArgs& a, RankScratch& rs, int& b
   return true;
 }
 
+// The rows of one wave in fp32 (RowWalk, the VALU decode arithmetic), for a
+// workgroup whose fp16 operands overflowed: rows w_first .. w_first + 31 of
+// sequence b, head h, keys [key_lo, key_hi) of the row's causal range.  It
+// writes what the matrix-core loop would have: the normalised output row, or
+// with a key-range split the part's un-normalised state.  One row at a time
+// with the whole wave on it: slow, and only taken for such inputs.
+template <typename T, int D>
+__device__ inline void prefill_rows_fp32(const PrefillArgs& a, int b, int h,
+                                                            int kvh, int row0, int S_b,
+                                                            int base_pos, int cap, int w_first,
+                                                            int key_lo, int key_hi, int part) {
+  using Walk = RowWalk<T, D, true, 1>;   // 16-token pages: a load group never straddles one
+  const KvPages kv{a.k, a.v, a.Hkv, 16, a.NB};
+  const int32_t* bt = a.bt + (int64_t)b * a.MB;
+  for (int j = 0; j < kRowsPerWave; ++j) {
+    const int i = w_first + j;
+    if (i >= S_b || (a.n_split > 1 && i >= a.rows_cap)) break;
+    const int hi = min(key_hi, min(base_pos + i, cap - 1) + 1);
+    const float* q = a.q + ((int64_t)(row0 + i) * a.H + h) * D;
+    Walk w;
+    if (key_lo < hi) {
+      w.run(kv, q, a.qscale, kvh, bt, key_lo, hi);
+    } else {   // no keys: a zero row, or an empty part (weight 0 in the merge)
+      w.m[0] = kNegBig;
+      w.l[0] = 0.0f;
+#pragma unroll
+      for (int e = 0; e < Walk::kVec; ++e) w.acc[0][e] = 0.0f;
+    }
+    if (a.n_split > 1) {
+      const int64_t pair = ((int64_t)(part * a.B + b) * a.rows_cap + i) * a.H + h;
+      w.store_state(0, a.part_o + pair * D, a.part_ml + pair);
+    } else {
+      w.store_out(0, a.out + ((int64_t)(row0 + i) * a.H + h) * D);
+    }
+  }
+}
+
 template <typename T, int D, int W>
 __global__ __launch_bounds__((Shape<D, W>::kThreads)) __attribute__((amdgpu_waves_per_eu(2)))
 void prefill_mfma_kernel(PrefillArgs a) {
@@ -331,6 +382,7 @@ void prefill_mfma_kernel(PrefillArgs a) {
   constexpr int kDB = D / 32;     // 32-dim output blocks
   constexpr int kNKB = kBN / 32;  // 32-key blocks per tile
   __shared__ PrefillTileLds<D> lds[2];
+  __shared__ int range_fail;      // some fp16 operand of this workgroup was inf or NaN
 
   // ---- which (sequence, head, query tile) -------------------------------
   int b, h, qt, row0, S_b, ctx_b, part = 0;
@@ -359,6 +411,7 @@ void prefill_mfma_kernel(PrefillArgs a) {
     ctx_b = a.ctx[b];
   }
   if (qt * kBM >= S_b) return;
+  if (threadIdx.x == 0) range_fail = 0;   // ordered before any write by the walk's barriers
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -426,6 +479,7 @@ void prefill_mfma_kernel(PrefillArgs a) {
     P pr;
     pr.init(a, wave, kvh);
     typename P::Regs rg;
+    float qchk = 0.0f;   // range check of this lane's fp16 query words
     // In the main loop every load and block-id fetch is unconditional, so that
     // the compiler counts outstanding loads exactly and waits only for the tile
     // it is about to store (a load issued under a condition makes it wait for
@@ -454,9 +508,10 @@ void prefill_mfma_kernel(PrefillArgs a) {
 #pragma unroll
       for (int c = 0; c < kDC16; ++c) {
         const float4 x0 = x[2 * c], x1 = x[2 * c + 1];
-        qf[c] = __builtin_bit_cast(
-            half8, make_uint4(pack_f16(x0.x * sc, x0.y * sc), pack_f16(x0.z * sc, x0.w * sc),
-                              pack_f16(x1.x * sc, x1.y * sc), pack_f16(x1.z * sc, x1.w * sc)));
+        const uint4 w = make_uint4(pack_f16(x0.x * sc, x0.y * sc), pack_f16(x0.z * sc, x0.w * sc),
+                                   pack_f16(x1.x * sc, x1.y * sc), pack_f16(x1.z * sc, x1.w * sc));
+        qchk = f16_check(w, qchk);
+        qf[c] = __builtin_bit_cast(half8, w);
       }
     }
     if constexpr (kProd) {
@@ -596,9 +651,20 @@ void prefill_mfma_kernel(PrefillArgs a) {
       tile_step(S1{}, Tail{}, kt);
       tile_step(S0{}, Tail{}, kt + 1);
     }
+    return f16_check_failed(pr.chk + qchk);
   };
-  if (wave < Sh::kProdWaves) run(std::true_type{});
-  else run(std::false_type{});
+  const bool my_fail = wave < Sh::kProdWaves ? run(std::true_type{}) : run(std::false_type{});
+
+  // Operands fp16 cannot hold (a bf16 K/V value of magnitude >= 65536 among the
+  // keys this workgroup walked, or a scaled query >= 65520) make the
+  // matrix-core result unusable: the workgroup recomputes its rows in fp32.
+  if (my_fail) range_fail = 1;
+  __syncthreads();
+  if (range_fail) {
+    prefill_rows_fp32<T, D>(a, b, h, kvh, row0, S_b, base_pos, cap, w_first, kt0 * kBN,
+                            kt1 * kBN, part);
+    return;
+  }
 
   // ---- normalise and store: lane (j, hh) owns query j and dims
   // d*32 + 8*g + 4*hh + (0..3) ----
