@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of hetero-serve's paged-attention hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps 50] [--warmup 5] [--config C2]
+    python bench.py [--gpus 1] [--steps 50] [--warmup 5] [--no-secondary] [--no-cpu]
 
 One step is one call of the decode attention (hs_decode: the partition
 kernel plus the log-sum-exp merge) over one layer of the whole batch, with
@@ -9,15 +9,27 @@ every input already resident in HBM.  The headline workload is configuration
 C2 (ragged decode, batch 64, 32 heads, head_dim 128, bf16 KV, block_size 16,
 context lognormal(median 2048, sigma 0.8) clipped to [64, 8192]); `value` is
 its algorithmic HBM throughput in GB/s (K and V of every context token read
-once, divided by the step time).  The JSON line also carries:
+once, divided by the step time).
 
-  roofline      the partition kernel alone, timed with HIP events that the
+Every leg is checked before its number counts, as the reference's benchmark
+does before timing (scripts/bench_kernel.py:193-201 for decode, :285-292 for
+prefill): attention outputs against the CPU oracle computed on the same inputs
+(max abs error <= 2e-3, the north-star bar; the reference gates at 2e-2 and
+3e-2), pack and unpack bit for bit.  The line carries each leg's error; when
+any check fails, "parity" is "fail" and the process exits with status 1.
+
+The JSON line also carries:
+
+  roofline      the dominant kernel alone, timed with HIP events that the
                 library records around that launch on its own stream, against
-                MI355X's 8 TB/s HBM peak
-  cpu_baseline  the CPU oracle (oracle/attention.py) timed on this host on a
-                seeded sample of C2's sequences
-  secondary     chunked prefill (C4) in TFLOP/s against the dense fp16 MFMA
-                peak, and the 4096-block migration pack of C5 in GB/s
+                MI355X's 8 TB/s HBM peak (or the 2.5 PFLOP/s dense fp16 MFMA
+                peak for prefill)
+  cpu_baseline  the CPU oracle (oracle/) on this host's cores, on the same
+                inputs, with the CPU model and thread count
+  secondary     C1 (small decode), C3 (long-context decode), C2 at Llama-3-8B's
+                grouped-query geometry, C4 chunked prefill, the C5 migration
+                pack and unpack of 4096 blocks with a plain-copy ceiling, the
+                C5 KV write and the C5 mixed step
 
 Only rank 0 of a one-GPU run exists: there is no multi-GPU path on this box.
 """
@@ -27,7 +39,6 @@ from __future__ import annotations
 import argparse
 import json
 import os
-import platform
 import statistics
 import sys
 import time
@@ -41,6 +52,7 @@ for _p in (ROOT, ROOT / "hetero-serve_amd"):
 METRIC = "decode µs/step + HBM GB/s (% peak); prefill TFLOP/s (% MFMA peak)"
 HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0
+TOL = 2e-3                     # north-star max abs error for fp16/bf16 caches
 
 
 def log(*a) -> None:
@@ -48,8 +60,9 @@ def log(*a) -> None:
 
 
 # HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE, WRITE_SIZE,
-# calibrated on a 1 GiB copy) for the default workload; summarised in the
-# committed profile below, whose table this reads.
+# calibrated on a 1 GiB copy) for the default workload, in a separate profiled
+# run of this script; summarised in the committed profile below, whose table
+# this reads.
 TRAFFIC_PROFILE = ROOT / "profiles" / "decode_C2_prefill_C4_pack_C5.md"
 # The headline leg's dominant kernel, as rocprofv3 names it.
 DECODE_KERNEL = "hs::row_attn_part_kernel<hs::Bf16, 128, true, 1>"
@@ -74,13 +87,58 @@ def profiled_traffic(kernel: str, workgroups: int):
     return None
 
 
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+
+    return platform.processor() or platform.machine()
+
+
+def host_threads() -> int:
+    return int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
+
+
+def roofline(kind: str, kernel: str, amount: float, kernel_ms: float, traffic=None) -> dict:
+    """achieved = algorithmic bytes (or FLOPs) of one launch / its mean time."""
+    if kind == "hbm":
+        achieved = amount / (kernel_ms * 1e-3) / 1e9
+        peak, unit = HBM_PEAK_GBS, "GB/s"
+    else:
+        achieved = amount / (kernel_ms * 1e-3) / 1e12
+        peak, unit = MFMA_F16_PEAK_TFLOPS, "TFLOP/s"
+    out = {"bound": kind, "kernel": kernel, "achieved": round(achieved, 2), "peak": peak,
+           "unit": unit, "frac": round(achieved / peak, 4), "traffic": traffic,
+           "algorithmic": int(amount), "kernel_us": round(kernel_ms * 1e3, 2)}
+    if traffic is not None:
+        out["traffic_source"] = (f"profiles/{TRAFFIC_PROFILE.name}: rocprofv3 --pmc FETCH_SIZE + "
+                                 "WRITE_SIZE of this launch in a profiled run of bench.py")
+    return out
+
+
+def median_time(fn, runs: int = 3) -> float:
+    """Median seconds of `runs` calls after one warm-up call."""
+    fn()
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts)
+
+
 # ---------------------------------------------------------------------------
 # GPU legs
 # ---------------------------------------------------------------------------
 
 
 def decode_leg(case, steps: int, warmup: int, partition_tokens: int = 0) -> dict:
-    """Time hs_decode on `case`; returns step/kernel times and throughputs."""
+    """Time hs_decode on `case`; returns step/kernel times, throughputs and the
+    output of the last step."""
     import torch
 
     from heteroserve import _hip
@@ -147,42 +205,162 @@ def prefill_leg(case, steps: int, warmup: int) -> dict:
     k_ms = statistics.mean(kernel_ms)
     return dict(step_ms=step_ms, kernel_ms=k_ms, flops=flops,
                 step_tflops=flops / (step_ms * 1e-3) / 1e12,
-                kernel_tflops=flops / (k_ms * 1e-3) / 1e12)
+                kernel_tflops=flops / (k_ms * 1e-3) / 1e12, out=out)
 
 
-def pack_leg(steps: int, warmup: int) -> dict:
+def _copy_timed(step, steps: int, warmup: int) -> tuple:
+    """(mean step ms, mean kernel ms) of a libhsattn copy call."""
     import torch
 
     from heteroserve import _hip
-    from hsbench import cases
     from hsbench.timing import time_steps
 
     lib = _hip.lib()
-    nb = cases.C5_POOL_BLOCKS
-    dev = "cuda:0"
-    pool = torch.empty((1, 2, nb, 16, 32, 128), dtype=torch.bfloat16, device=dev)
-    cases._fill_pool(pool, torch.Generator(device=dev).manual_seed(41))
-    ids = torch.as_tensor(cases.c5_pack_ids(nb), dtype=torch.int64, device=dev)
-    out = torch.empty((ids.numel(), 1, 2, 16, 32, 128), dtype=torch.bfloat16, device=dev)
-    page = pool[0, 0, 0].numel() * pool.element_size()
     stream = torch.cuda.current_stream().cuda_stream
-
-    def step():
-        _hip.check(lib.hs_kv_pack(pool.data_ptr(), 1, nb, page, ids.data_ptr(), ids.numel(),
-                                  out.data_ptr(), stream))
 
     def arm(s, e):
         _hip.check(lib.hs_profile_next_launch(s.handle, e.handle))
 
     step_ms, kernel_ms, _ = time_steps(step, steps, warmup, stream, arm)
-    want = pool[:, :, ids].permute(2, 0, 1, 3, 4, 5)
-    exact = bool(torch.equal(out.view(torch.int16), want.contiguous().view(torch.int16)))
+    return step_ms, statistics.mean(kernel_ms)
+
+
+def migration_legs(steps: int, warmup: int, with_cpu: bool) -> dict:
+    """C5's migration copies on one pool [1, 2, 65536, 16, 32, 128] bf16 (17.2 GB):
+    the pack of 4096 random blocks (1 GiB payload, export_blocks_device,
+    torch_blocks.py:137-148), its unpack into another pool at the same ids
+    (write_blocks_device, :150-154), and two plain-copy ceilings of the same
+    1 GiB (torch's contiguous copy_, and the pack kernel on 4096 consecutive
+    blocks).  The pack is checked bit for bit against the CPU torch oracle
+    (the reference's own expression on a host copy of the pool) and the
+    unpack against torch's GPU indexing; the CPU forms are also timed."""
+    import torch
+
+    from heteroserve import _hip
+    from hsbench import cases
+    from hsbench.timing import Event
+
+    lib = _hip.lib()
+    nb = cases.C5_POOL_BLOCKS
+    dev = "cuda:0"
+    stream = torch.cuda.current_stream().cuda_stream
+    pool = torch.empty((1, 2, nb, 16, 32, 128), dtype=torch.bfloat16, device=dev)
+    cases._fill_pool(pool, torch.Generator(device=dev).manual_seed(41))
+    id_list = cases.c5_pack_ids(nb)
+    ids = torch.as_tensor(id_list, dtype=torch.int64, device=dev)
+    n = ids.numel()
+    out = torch.empty((n, 1, 2, 16, 32, 128), dtype=torch.bfloat16, device=dev)
+    page = pool[0, 0, 0].numel() * pool.element_size()
     nbytes = 2 * out.numel() * out.element_size()      # read + write
-    k_ms = statistics.mean(kernel_ms)
-    del pool, out, want
+
+    def pack():
+        _hip.check(lib.hs_kv_pack(pool.data_ptr(), 1, nb, page, ids.data_ptr(), n,
+                                  out.data_ptr(), stream))
+
+    pk_step, pk_kernel = _copy_timed(pack, steps, warmup)
+    res = {"pack": {"us_per_step": round(pk_step * 1e3, 2),
+                    "gbs": round(nbytes / (pk_kernel * 1e-3) / 1e9, 1),
+                    "bytes_moved": nbytes,
+                    "roofline": roofline("hbm", "page_copy_kernel", nbytes, pk_kernel)}}
+    log(f"C5 pack: {pk_kernel * 1e3:.1f} us, {res['pack']['gbs']:.0f} GB/s")
+
+    # unpack into a zeroed pool at the same ids
+    dst = torch.zeros_like(pool)
+
+    def unpack():
+        _hip.check(lib.hs_kv_unpack(dst.data_ptr(), 1, nb, page, ids.data_ptr(), n,
+                                    out.data_ptr(), stream))
+
+    up_step, up_kernel = _copy_timed(unpack, steps, warmup)
+    got = dst[:, :, ids].permute(2, 0, 1, 3, 4, 5)
+    up_exact = bool(torch.equal(got.contiguous().view(torch.int16), out.view(torch.int16)))
+    dst.index_fill_(2, ids, 0)
+    up_exact = up_exact and not bool(dst.view(torch.int16).any())     # nothing else written
+    del dst, got
+    res["unpack"] = {"us_per_step": round(up_step * 1e3, 2),
+                     "gbs": round(nbytes / (up_kernel * 1e-3) / 1e9, 1),
+                     "bytes_moved": nbytes, "bit_exact": up_exact,
+                     "check": "torch GPU indexing of the unpacked pool == payload; "
+                              "every other block untouched",
+                     "roofline": roofline("hbm", "page_copy_kernel", nbytes, up_kernel)}
+    log(f"C5 unpack: {up_kernel * 1e3:.1f} us, {res['unpack']['gbs']:.0f} GB/s, exact={up_exact}")
+
+    # plain-copy ceilings of the same 1 GiB (into their own buffer: `out`
+    # keeps the payload for the checks below)
+    seq = torch.arange(n, dtype=torch.int64, device=dev)
+    seq_out = torch.empty_like(out)
+
+    def pack_seq():
+        _hip.check(lib.hs_kv_pack(pool.data_ptr(), 1, nb, page, seq.data_ptr(), n,
+                                  seq_out.data_ptr(), stream))
+
+    _, seq_kernel = _copy_timed(pack_seq, steps, warmup)
+    src = pool[0, :, :n // 2].contiguous()               # 1 GiB, contiguous
+    cdst = torch.empty_like(src)
+    for _ in range(warmup):
+        cdst.copy_(src)
+    e0, e1 = Event(), Event()
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(steps):
+        cdst.copy_(src)
+    e1.record(stream)
+    copy_ms = e0.elapsed_ms(e1) / steps
+    cbytes = 2 * src.numel() * src.element_size()
+    res["copy_ceiling"] = {
+        "pack_consecutive_blocks_gbs": round(nbytes / (seq_kernel * 1e-3) / 1e9, 1),
+        "torch_copy_gbs": round(cbytes / (copy_ms * 1e-3) / 1e9, 1),
+        "bytes_moved": nbytes,
+        "note": "the same 1 GiB read + written: the pack kernel on blocks 0..4095, and "
+                "torch's contiguous copy_ (a step, not a kernel event)"}
+    log(f"copy ceilings: pack of consecutive blocks {res['copy_ceiling']['pack_consecutive_blocks_gbs']}"
+        f" GB/s, torch copy_ {res['copy_ceiling']['torch_copy_gbs']} GB/s")
+    del src, cdst, seq_out
+
+    if with_cpu:
+        from oracle.kvpack import export_blocks_torch, write_blocks_torch
+
+        torch.set_num_threads(host_threads())
+        hpool = pool.cpu()
+        del pool
+        torch.cuda.empty_cache()
+        payload = {}
+
+        def cpu_pack():
+            payload["x"] = export_blocks_torch(hpool, id_list)
+
+        t_pack = median_time(cpu_pack)
+        exact = bool(torch.equal(out.cpu().view(torch.int16), payload["x"].view(torch.int16)))
+        res["pack"]["bit_exact"] = exact
+        res["pack"]["check"] = "GPU payload == CPU torch oracle payload, bit for bit"
+        res["pack"]["cpu_baseline"] = {
+            "value": round(nbytes / t_pack / 1e9, 3), "unit": "GB/s",
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": (f"the whole C5 pack (4096 random blocks of a 65536-block host pool, "
+                       f"1 GiB payload): oracle/kvpack.py export_blocks_torch, the reference's "
+                       f"pool[:, :, idx].permute(2, 0, 1, 3, 4, 5).contiguous() in torch on "
+                       f"{torch.get_num_threads()} threads, median of 3 after 1 warm-up: "
+                       f"{t_pack * 1e3:.1f} ms; cpu={cpu_model()}")}
+        x = payload["x"]
+        t_unpack = median_time(lambda: write_blocks_torch(hpool, id_list, x))
+        res["unpack"]["cpu_baseline"] = {
+            "value": round(nbytes / t_unpack / 1e9, 3), "unit": "GB/s",
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": (f"the whole C5 unpack (4096 blocks of 256 KiB into the host pool): "
+                       f"oracle/kvpack.py write_blocks_torch, the reference's per-block loop "
+                       f"pool[:, :, blk] = data[i] in torch, median of 3 after 1 warm-up: "
+                       f"{t_unpack * 1e3:.1f} ms; cpu={cpu_model()}")}
+        log(f"C5 pack cpu: {res['pack']['cpu_baseline']['value']} GB/s, exact={exact}; "
+            f"unpack cpu: {res['unpack']['cpu_baseline']['value']} GB/s")
+        del hpool, payload, x
+    else:
+        want = pool[:, :, ids].permute(2, 0, 1, 3, 4, 5).contiguous()
+        res["pack"]["bit_exact"] = bool(torch.equal(out.view(torch.int16), want.view(torch.int16)))
+        res["pack"]["check"] = "GPU payload == torch GPU indexing, bit for bit (no CPU leg)"
+        del pool, want
+    del out
     torch.cuda.empty_cache()
-    return dict(step_ms=step_ms, kernel_ms=k_ms, bytes=nbytes, bit_exact=exact,
-                kernel_gbs=nbytes / (k_ms * 1e-3) / 1e9, step_gbs=nbytes / (step_ms * 1e-3) / 1e9)
+    return res
 
 
 def kv_write_leg(steps: int, warmup: int) -> dict:
@@ -211,8 +389,8 @@ def kv_write_leg(steps: int, warmup: int) -> dict:
     k, v = qkv[:, kvd:2 * kvd], qkv[:, 2 * kvd:]
     stream = torch.cuda.current_stream().cuda_stream
     args = (kc.data_ptr(), vc.data_ptr(), _hip.dtype_code(kc.dtype), nb, bs, h, d, bt.data_ptr(),
-            bt.shape[1], pos.data_ptr(), seq.data_ptr(), T, k.data_ptr(), v.data_ptr(),
-            _hip.DTYPE_F32, qkv.stride(0), stream)
+            bt.shape[0], bt.shape[1], pos.data_ptr(), seq.data_ptr(), T, k.data_ptr(),
+            v.data_ptr(), _hip.DTYPE_F32, qkv.stride(0), stream)
 
     def step():
         _hip.check(lib.hs_kv_append(*args))
@@ -298,8 +476,8 @@ def c5_step_leg(steps: int, warmup: int) -> dict:
     parts = {
         "kv_write_chunk": lambda: lib.hs_kv_append(
             pkc.data_ptr(), pvc.data_ptr(), kdt, pnb, bs, hkv, D, pc.block_tables.data_ptr(),
-            pc.block_tables.shape[1], ppos.data_ptr(), pseq.data_ptr(), T,
-            qkv_p[:, kvd:].data_ptr(), qkv_p[:, 2 * kvd:].data_ptr(), f32, qkv_p.stride(0),
+            pc.block_tables.shape[0], pc.block_tables.shape[1], ppos.data_ptr(), pseq.data_ptr(),
+            T, qkv_p[:, kvd:].data_ptr(), qkv_p[:, 2 * kvd:].data_ptr(), f32, qkv_p.stride(0),
             stream),
         "prefill": lambda: lib.hs_prefill_varlen(
             pc.q.data_ptr(), pc.cu_seqlens.data_ptr(), T, pkc.data_ptr(), pvc.data_ptr(), kdt,
@@ -307,8 +485,8 @@ def c5_step_leg(steps: int, warmup: int) -> dict:
             hkv, D, bs, pc.block_tables.shape[1], float(pc.scale), 1,
             pws.data_ptr() if pws is not None else None, pws_bytes, stream),
         "kv_write_decode": lambda: lib.hs_kv_append(
-            dkc.data_ptr(), dvc.data_ptr(), kdt, dnb, bs, hkv, D, dc.block_tables.data_ptr(), dmb,
-            dpos.data_ptr(), dseq.data_ptr(), B, qkv_d[:, kvd:].data_ptr(),
+            dkc.data_ptr(), dvc.data_ptr(), kdt, dnb, bs, hkv, D, dc.block_tables.data_ptr(), B,
+            dmb, dpos.data_ptr(), dseq.data_ptr(), B, qkv_d[:, kvd:].data_ptr(),
             qkv_d[:, 2 * kvd:].data_ptr(), f32, qkv_d.stride(0), stream),
         "decode": lambda: lib.hs_decode_shared(
             dc.q.data_ptr(), dkc.data_ptr(), dvc.data_ptr(), kdt, dnb,
@@ -361,70 +539,89 @@ def c5_step_leg(steps: int, warmup: int) -> dict:
 
 
 # ---------------------------------------------------------------------------
-# CPU baseline: the oracle on this host's cores
+# CPU baselines: the oracle on this host's cores, on the same inputs; their
+# outputs are the parity reference of the GPU legs
 # ---------------------------------------------------------------------------
 
 
-def cpu_baseline(case, n_seq: int = 0, seed: int = 7) -> dict:
-    """Per-sequence torch oracle over the case's sequences (all of them when
-    n_seq is 0, else a seeded sample of n_seq)."""
+def cpu_decode_baseline(case, n_seq: int = 0, seed: int = 7):
+    """Per-sequence torch oracle (oracle/attention.py decode_one) over the
+    case's sequences, all of them when n_seq is 0, else a seeded sample of
+    n_seq; returns (baseline dict, {sequence: oracle output})."""
     import numpy as np
     import torch
 
     from oracle.attention import decode_one
 
-    threads = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
-    torch.set_num_threads(threads)
+    torch.set_num_threads(host_threads())
     rng = np.random.default_rng(seed)
     n_pick = len(case.ctx) if n_seq <= 0 else min(n_seq, len(case.ctx))
-    pick = sorted(rng.choice(len(case.ctx), size=n_pick, replace=False))
-    host = []
+    pick = sorted(rng.choice(len(case.ctx), size=n_pick, replace=False).tolist())
+    total, outs = 0.0, {}
     for b in pick:
         n = int(case.ctx[b])
         nblk = -(-n // 16)
         blocks = case.block_tables[b, :nblk].long()
-        host.append((case.q[b].cpu(), case.k_cache.index_select(0, blocks).cpu(),
-                     case.v_cache.index_select(0, blocks).cpu(),
-                     torch.arange(nblk, dtype=torch.int32), n))
-    total = 0.0
-    for q, kb, vb, tbl, n in host:
-        decode_one(q, kb, vb, tbl, n, case.scale)           # warm-up
-        runs = []
-        for _ in range(3):
-            t0 = time.perf_counter()
-            decode_one(q, kb, vb, tbl, n, case.scale)
-            runs.append(time.perf_counter() - t0)
-        total += statistics.median(runs)
+        q, kb, vb = (case.q[b].cpu(), case.k_cache.index_select(0, blocks).cpu(),
+                     case.v_cache.index_select(0, blocks).cpu())
+        tbl = torch.arange(nblk, dtype=torch.int32)
+        total += median_time(lambda: outs.__setitem__(b, decode_one(q, kb, vb, tbl, n,
+                                                                    case.scale)))
     tokens = int(sum(int(case.ctx[b]) for b in pick))
     nbytes = tokens * case.row_bytes()
+    what = "all" if n_pick == len(case.ctx) else f"a seeded sample of {n_pick} of the"
     return {
         "value": round(nbytes / total / 1e9, 3),
         "unit": "GB/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": (f"{len(pick)} seeded {case.name} sequences ({tokens} of "
+        "sample": (f"{what} {len(case.ctx)} {case.name} sequences ({tokens} of "
                    f"{int(case.ctx.sum())} context tokens), oracle/attention.py decode_one "
-                   f"(torch fp32 CPU), median of 3 after 1 warm-up, summed: "
-                   f"{total * 1e3:.1f} ms for {nbytes / 1e6:.1f} MB of K+V; "
-                   f"cpu={platform.processor() or platform.machine()}"),
-    }
+                   f"(torch fp32 CPU) per sequence, median of 3 after 1 warm-up, summed: "
+                   f"{total * 1e3:.1f} ms for {nbytes / 1e6:.1f} MB of K+V (a rate, so the "
+                   f"sample's bytes over the sample's time); cpu={cpu_model()}"),
+    }, outs
 
 
-def cpu_prefill_baseline(case, heads: int = 0) -> dict:
+def cpu_decode_batched(case):
+    """The batched torch oracle (oracle/attention.py paged_attention_torch, the
+    reference's paged_attention_torch) over the whole case in one call, as the
+    reference computes it on the CPU; returns (baseline dict, output)."""
+    import torch
+
+    from oracle.attention import paged_attention_torch
+
+    torch.set_num_threads(host_threads())
+    args = [t.cpu() for t in (case.q, case.k_cache, case.v_cache, case.block_tables,
+                              case.context_lens)]
+    res = {}
+    t = median_time(lambda: res.__setitem__("out", paged_attention_torch(*args, case.scale)))
+    nbytes = case.decode_bytes()
+    return {
+        "value": round(nbytes / t / 1e9, 3), "unit": "GB/s", "cores": torch.get_num_threads(),
+        "kind": "port", "us_per_step": round(t * 1e6, 1),
+        "sample": (f"the whole {case.name} batch ({len(case.ctx)} sequences) in one call of "
+                   f"oracle/attention.py paged_attention_torch (torch fp32 CPU), median of 3 "
+                   f"after 1 warm-up: {t * 1e3:.2f} ms for {nbytes / 1e6:.2f} MB of K+V; "
+                   f"cpu={cpu_model()}"),
+    }, res["out"]
+
+
+def cpu_prefill_baseline(case, heads: int = 0):
     """The prefill oracle (oracle/attention.py prefill_one, the reference's
     paged_attention_prefill_torch per sequence) over every sequence of the
     case for `heads` of its heads (all of them when 0); useful causal FLOPs of
-    that sample over the summed median times."""
+    that sample over the summed median times.  Returns (baseline dict,
+    {sequence: oracle output [S_b, heads, D]})."""
     import torch
 
     from oracle.attention import prefill_one
 
-    threads = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
-    torch.set_num_threads(threads)
+    torch.set_num_threads(host_threads())
     D = case.head_dim
     heads = heads or case.n_heads
     cu = case.cu_seqlens.cpu().tolist()
-    total, flops = 0.0, 0
+    total, flops, outs = 0.0, 0, {}
     for b in range(len(case.ctx)):
         n, S = int(case.ctx[b]), cu[b + 1] - cu[b]
         nblk = -(-n // 16)
@@ -433,13 +630,8 @@ def cpu_prefill_baseline(case, heads: int = 0) -> dict:
         kb = case.k_cache.index_select(0, blocks)[:, :, :heads].cpu()
         vb = case.v_cache.index_select(0, blocks)[:, :, :heads].cpu()
         tbl = torch.arange(nblk, dtype=torch.int32)
-        prefill_one(q, kb, vb, tbl, n, case.scale)           # warm-up
-        runs = []
-        for _ in range(3):
-            t0 = time.perf_counter()
-            prefill_one(q, kb, vb, tbl, n, case.scale)
-            runs.append(time.perf_counter() - t0)
-        total += statistics.median(runs)
+        total += median_time(lambda: outs.__setitem__(b, prefill_one(q, kb, vb, tbl, n,
+                                                                     case.scale)))
         P = n - S
         flops += 4 * heads * D * (S * P + S * (S + 1) // 2)
     return {
@@ -447,39 +639,76 @@ def cpu_prefill_baseline(case, heads: int = 0) -> dict:
         "cores": torch.get_num_threads(), "kind": "port",
         "sample": (f"all {len(case.ctx)} {case.name} sequences, {heads} of {case.n_heads} heads, "
                    f"oracle/attention.py prefill_one (torch fp32 CPU), median of 3 after 1 "
-                   f"warm-up, summed: {total * 1e3:.1f} ms for {flops / 1e9:.2f} useful GFLOP"),
-    }
+                   f"warm-up, summed: {total * 1e3:.1f} ms for {flops / 1e9:.2f} useful GFLOP; "
+                   f"cpu={cpu_model()}"),
+    }, outs
 
 
-def cpu_pack_baseline(n: int = 1024, pool_blocks: int = 2048, seed: int = 43) -> dict:
-    """The pack oracle (oracle/kvpack.py export_blocks, the reference's
-    pool[:, :, idx].permute(2, 0, 1, ...).contiguous() in numpy) gathering n
-    random blocks of C5's page shape from a host pool; read + write bytes."""
-    import numpy as np
+def max_err_decode(got, outs: dict) -> float:
+    return max((got[b].detach().cpu() - w).abs().max().item() for b, w in outs.items())
 
-    from oracle.kvpack import export_blocks
 
-    rng = np.random.default_rng(seed)
-    pool = rng.integers(0, 1 << 16, size=(1, 2, pool_blocks, 16, 32, 128), dtype=np.uint16)
-    ids = rng.choice(pool_blocks, size=n, replace=False).tolist()
-    export_blocks(pool, ids)                                 # warm-up
-    runs = []
-    for _ in range(3):
-        t0 = time.perf_counter()
-        out = export_blocks(pool, ids)
-        runs.append(time.perf_counter() - t0)
-    t = statistics.median(runs)
-    nbytes = 2 * out.nbytes
-    return {
-        "value": round(nbytes / t / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
-        "sample": (f"{n} random blocks of [1, 2, 16, 32, 128] 16-bit elements from a "
-                   f"{pool_blocks}-block host pool, oracle/kvpack.py export_blocks (numpy), "
-                   f"median of 3 after 1 warm-up: {t * 1e3:.1f} ms for {nbytes / 1e6:.0f} MB "
-                   f"read + written"),
-    }
+def max_err_prefill(case, got, outs: dict, heads: int = 0) -> float:
+    cu = case.cu_seqlens.cpu().tolist()
+    heads = heads or case.n_heads
+    return max((got[cu[b]:cu[b + 1], :heads].detach().cpu() - w).abs().max().item()
+               for b, w in outs.items())
 
 
 # ---------------------------------------------------------------------------
+
+
+def decode_config(case, partition: int) -> dict:
+    kv_dtype = str(case.k_cache.dtype).replace("torch.", "")
+    cfg = {
+        "workload": f"{case.name} paged decode, one layer",
+        "batch": len(case.ctx), "heads": case.n_heads, "kv_heads": case.kv_heads,
+        "head_dim": case.head_dim, "block_size": 16, "kv_dtype": kv_dtype,
+        "sum_context": int(case.ctx.sum()), "max_context": int(case.ctx.max()),
+        "num_blocks": int(case.k_cache.shape[0]),
+        "decomposition": (f"fixed partitions of {partition} tokens + LSE merge"
+                          if partition else
+                          "library default partitions (512 tokens, halved down to 32 while "
+                          "the grid has fewer than 4 waves per CU) + LSE merge"),
+        "parallelism": "none (one GPU)",
+    }
+    if case.meta.get("shared_blocks"):
+        cfg["unique_bytes"] = case.unique_decode_bytes()
+    return cfg
+
+
+def secondary_decode(name: str, kernel: str, steps: int, warmup: int, with_cpu: bool,
+                     batched_cpu: bool = False, n_seq: int = 0) -> dict:
+    """One more decode configuration: step time, roofline of its partition
+    kernel, CPU baseline and parity against the oracle outputs."""
+    import torch
+
+    from hsbench import cases
+
+    case = cases.CONFIGS[name]("cuda:0")
+    dec = decode_leg(case, steps, warmup)
+    res = {"us_per_step": round(dec["step_ms"] * 1e3, 2), "gbs": round(dec["step_gbs"], 1),
+           "hbm_frac": round(dec["step_gbs"] / HBM_PEAK_GBS, 4),
+           "config": decode_config(case, 0),
+           "roofline": roofline("hbm", kernel, dec["bytes"], dec["kernel_ms"])}
+    log(f"{name} decode: step {dec['step_ms'] * 1e3:.1f} us ({dec['step_gbs']:.0f} GB/s), "
+        f"kernel {dec['kernel_ms'] * 1e3:.1f} us ({dec['kernel_gbs']:.0f} GB/s)")
+    if with_cpu:
+        if batched_cpu:
+            cpu, want = cpu_decode_batched(case)
+            err = (dec["out"].cpu() - want).abs().max().item()
+            res["parity_sample"] = "every sequence"
+        else:
+            cpu, outs = cpu_decode_baseline(case, n_seq=n_seq)
+            err = max_err_decode(dec["out"], outs)
+            res["parity_sample"] = (f"{len(outs)} of {len(case.ctx)} sequences (the CPU "
+                                    "baseline's sample)")
+        res["cpu_baseline"] = cpu
+        res["max_abs_err"] = err
+        log(f"{name} cpu baseline: {cpu['value']} GB/s; max abs err {err:.2e}")
+    del case, dec
+    torch.cuda.empty_cache()
+    return res
 
 
 def main() -> int:
@@ -487,12 +716,14 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="C2", choices=["C1", "C2", "C3", "C5-decode"],
+    ap.add_argument("--config", default="C2", choices=["C1", "C2", "C2-gqa", "C3", "C5-decode"],
                     help="decode configuration of the headline line")
     ap.add_argument("--partition", type=int, default=0,
                     help="decode partition tokens (0 = library default)")
-    ap.add_argument("--no-secondary", action="store_true", help="skip the C4 / C5 pack legs")
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-secondary", action="store_true", help="skip the secondary legs")
+    ap.add_argument("--no-cpu", action="store_true",
+                    help="skip the CPU baselines (and with them the parity checks of the "
+                         "attention legs)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -509,7 +740,11 @@ def main() -> int:
         log(f"libhsattn unavailable: {_hip.error()}")
         return 1
     dev = "cuda:0"
-    log(f"device: {torch.cuda.get_device_name(0)}")
+    log(f"device: {torch.cuda.get_device_name(0)}; host: {cpu_model()}, "
+        f"{host_threads()} threads")
+    with_cpu = not args.no_cpu
+    errors = {}          # leg -> max abs error (attention legs)
+    exact = {}           # leg -> bit-exact (copy legs)
 
     case = cases.CONFIGS[args.config](dev)
     log(f"{case.name}: B={len(case.ctx)} sum(ctx)={int(case.ctx.sum())} "
@@ -517,69 +752,72 @@ def main() -> int:
     dec = decode_leg(case, args.steps, args.warmup, args.partition)
     log(f"decode: step {dec['step_ms'] * 1e3:.1f} us ({dec['step_gbs']:.0f} GB/s), "
         f"partition kernel {dec['kernel_ms'] * 1e3:.1f} us ({dec['kernel_gbs']:.0f} GB/s)")
-
-    cpu = None if args.no_cpu else cpu_baseline(case)
-    if cpu:
-        log(f"cpu baseline: {cpu['value']} GB/s on {cpu['cores']} threads")
-
-    kv_dtype = str(case.k_cache.dtype).replace("torch.", "")
-    config = {
-        "workload": f"{case.name} paged decode, one layer",
-        "batch": len(case.ctx), "heads": case.n_heads, "kv_heads": case.kv_heads,
-        "head_dim": case.head_dim, "block_size": 16, "kv_dtype": kv_dtype,
-        "sum_context": int(case.ctx.sum()), "max_context": int(case.ctx.max()),
-        "num_blocks": int(case.k_cache.shape[0]),
-        "decomposition": (f"fixed partitions of {args.partition} tokens + LSE merge"
-                          if args.partition else
-                          "library default partitions (512 tokens, halved down to 32 while "
-                          "the grid has fewer than 4 waves per CU) + LSE merge"),
-        "parallelism": "none (one GPU)",
-    }
-    if case.meta.get("shared_blocks"):
-        config["unique_bytes"] = case.unique_decode_bytes()
+    cpu = None
+    if with_cpu:
+        cpu, outs = cpu_decode_baseline(case)
+        errors[case.name] = max_err_decode(dec["out"], outs)
+        log(f"cpu baseline: {cpu['value']} GB/s on {cpu['cores']} threads; "
+            f"max abs err {errors[case.name]:.2e}")
+        del outs
+    config = decode_config(case, args.partition)
+    headline_name = case.name
     del case
     torch.cuda.empty_cache()
 
     secondary = {}
     if not args.no_secondary:
-        try:
-            pc = cases.c4_prefill(dev)
-            # >= 60 warm-up launches (~20 ms): after the memory-bound decode leg
-            # the clock takes tens of milliseconds of MFMA work to ramp up
-            pre = prefill_leg(pc, max(20, args.steps // 5), max(60, args.warmup))
-            secondary["C4_prefill"] = {
-                "us_per_step": round(pre["step_ms"] * 1e3, 2),
-                "tflops": round(pre["step_tflops"], 2),
-                "kernel_tflops": round(pre["kernel_tflops"], 2),
-                "mfma_frac": round(pre["kernel_tflops"] / MFMA_F16_PEAK_TFLOPS, 4),
-                "useful_flops": pre["flops"],
-            }
-            log(f"C4 prefill: {pre['step_ms'] * 1e3:.1f} us, {pre['kernel_tflops']:.1f} TFLOP/s")
-            if not args.no_cpu:
-                secondary["C4_prefill"]["cpu_baseline"] = cpu_prefill_baseline(pc)
-                log(f"C4 prefill cpu baseline: "
-                    f"{secondary['C4_prefill']['cpu_baseline']['value']} TFLOP/s")
-            del pc
-        except RuntimeError as exc:
-            secondary["C4_prefill"] = {"error": str(exc)[:200]}
-        torch.cuda.empty_cache()
-        pk = pack_leg(max(5, args.steps // 5), 2)
-        secondary["C5_pack"] = {
-            "us_per_step": round(pk["step_ms"] * 1e3, 2), "gbs": round(pk["kernel_gbs"], 1),
-            "hbm_frac": round(pk["kernel_gbs"] / HBM_PEAK_GBS, 4), "bit_exact": pk["bit_exact"],
-            "bytes_moved": pk["bytes"],
+        legs = [("C1", "row_attn_part_kernel<_Float16, 64, true, 1>", True, 0),
+                ("C3", "row_attn_part_kernel<Bf16, 128, true, 1>", False, 4),
+                ("C2-gqa", "row_attn_part_kernel<Bf16, 128, true, 4>", False, 16)]
+        for name, kernel, batched, n_seq in legs:
+            if name == headline_name:
+                continue
+            r = secondary_decode(name, kernel, args.steps, args.warmup, with_cpu,
+                                 batched_cpu=batched, n_seq=n_seq)
+            secondary[f"{name}_decode"] = r
+            if "max_abs_err" in r:
+                errors[name] = r["max_abs_err"]
+
+        pc = cases.c4_prefill(dev)
+        # >= 60 warm-up launches (~20 ms): after the memory-bound decode legs
+        # the clock takes tens of milliseconds of MFMA work to ramp up
+        pre = prefill_leg(pc, max(20, args.steps // 5), max(60, args.warmup))
+        secondary["C4_prefill"] = {
+            "us_per_step": round(pre["step_ms"] * 1e3, 2),
+            "tflops": round(pre["step_tflops"], 2),
+            "kernel_tflops": round(pre["kernel_tflops"], 2),
+            "mfma_frac": round(pre["kernel_tflops"] / MFMA_F16_PEAK_TFLOPS, 4),
+            "useful_flops": pre["flops"],
+            "roofline": roofline("mfma", "prefill_mfma_kernel<Bf16, 128, 8>", pre["flops"],
+                                 pre["kernel_ms"]),
         }
-        log(f"C5 pack: {pk['kernel_ms'] * 1e3:.1f} us, {pk['kernel_gbs']:.0f} GB/s, "
-            f"exact={pk['bit_exact']}")
-        if not args.no_cpu:
-            secondary["C5_pack"]["cpu_baseline"] = cpu_pack_baseline()
-            log(f"C5 pack cpu baseline: {secondary['C5_pack']['cpu_baseline']['value']} GB/s")
+        log(f"C4 prefill: {pre['step_ms'] * 1e3:.1f} us, {pre['kernel_tflops']:.1f} TFLOP/s")
+        if with_cpu:
+            pcpu, pouts = cpu_prefill_baseline(pc)
+            secondary["C4_prefill"]["cpu_baseline"] = pcpu
+            errors["C4"] = max_err_prefill(pc, pre["out"], pouts)
+            secondary["C4_prefill"]["max_abs_err"] = errors["C4"]
+            secondary["C4_prefill"]["parity_sample"] = "every row of every sequence, all heads"
+            log(f"C4 prefill cpu baseline: {pcpu['value']} TFLOP/s; "
+                f"max abs err {errors['C4']:.2e}")
+            del pouts
+        del pc, pre
+        torch.cuda.empty_cache()
+
+        mig = migration_legs(max(5, args.steps // 5), 2, with_cpu)
+        secondary["C5_pack"] = mig["pack"]
+        secondary["C5_unpack"] = mig["unpack"]
+        secondary["copy_ceiling"] = mig["copy_ceiling"]
+        exact["C5_pack"] = mig["pack"]["bit_exact"]
+        exact["C5_unpack"] = mig["unpack"]["bit_exact"]
+
         kw = kv_write_leg(max(20, args.steps // 5), 10)
         secondary["C5_kv_write"] = {
             "us_per_step": round(kw["step_ms"] * 1e3, 2), "gbs": round(kw["kernel_gbs"], 1),
             "hbm_frac": round(kw["kernel_gbs"] / HBM_PEAK_GBS, 4), "bit_exact": kw["bit_exact"],
             "bytes_moved": kw["bytes"], "torch_index_put_us": round(kw["ref_ms"] * 1e3, 2),
         }
+        exact["C5_kv_write"] = kw["bit_exact"]
         log(f"C5 KV write (1024-token chunk): {kw['kernel_ms'] * 1e3:.1f} us, "
             f"{kw['kernel_gbs']:.0f} GB/s, torch fk[slots]=k: {kw['ref_ms'] * 1e3:.1f} us, "
             f"exact={kw['bit_exact']}")
@@ -589,6 +827,7 @@ def main() -> int:
             f"{k} {v['us']:.1f} us" for k, v in st["parts"].items())
             + f" (plain hs_decode: {st['decode_plain_us']:.1f} us)")
 
+    ok = all(e <= TOL for e in errors.values()) and all(exact.values())
     line = {
         "metric": METRIC,
         "value": round(dec["step_gbs"], 2),
@@ -605,23 +844,23 @@ def main() -> int:
         "dtype": "f32",
         "data": "synthetic (seeded N(0,1) KV and queries, seeded block tables)",
         "config": config,
-        "roofline": {
-            "bound": "hbm",
-            "kernel": "row_attn_part_kernel",
-            "achieved": round(dec["kernel_gbs"], 2),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(dec["kernel_gbs"] / HBM_PEAK_GBS, 4),
-            "traffic": profiled_traffic(DECODE_KERNEL, DECODE_WORKGROUPS)
-            if args.config == "C2" and not args.partition else None,
-            "traffic_source": TRAFFIC_PROFILE.name,
-            "algorithmic_bytes": dec["bytes"],
-            "kernel_us": round(dec["kernel_ms"] * 1e3, 2),
-        },
+        "roofline": roofline(
+            "hbm", "row_attn_part_kernel", dec["bytes"], dec["kernel_ms"],
+            profiled_traffic(DECODE_KERNEL, DECODE_WORKGROUPS)
+            if args.config == "C2" and not args.partition else None),
         "cpu_baseline": cpu,
+        "max_abs_err": errors.get(headline_name),
+        "parity": ("pass" if ok else "fail") if (errors or exact) else "not checked (--no-cpu)",
+        "parity_tolerance": TOL,
+        "parity_errors": {k: float(f"{v:.3e}") for k, v in errors.items()},
+        "parity_exact": exact,
+        "host": {"cpu": cpu_model(), "threads": host_threads()},
         "secondary": secondary,
     }
     print(json.dumps(line), flush=True)
+    if not ok:
+        log(f"parity check failed: errors {errors} (tolerance {TOL}), exact {exact}")
+        return 1
     return 0
 
 

@@ -6,6 +6,7 @@ The configurations are the reference path's headline workloads, restated:
       Q/K/V ~ N(0, 1) / sqrt(D)
   C2  ragged decode, B 64, 32 heads, D 128, bf16, ctx lognormal(median 2048,
       sigma 0.8) clipped to [64, 8192], 65536-block pool
+  C2-gqa  C2's batch at Llama-3-8B's geometry: 32 query heads on 8 KV heads
   C3  long-context decode, B 16, 32 heads, D 128, bf16, ctx U[8192, 32768]
   C4  chunked causal prefill, 8 sequences with a cached prefix U[0, 4096] and a
       new chunk U[128, 2048], 32 heads, D 128, bf16
@@ -214,6 +215,16 @@ def c2_decode(device, dtype=None) -> PagedCase:
                         device, 1, rng=rng)
 
 
+def c2_gqa_decode(device, dtype=None) -> PagedCase:
+    """C2's batch and contexts at Llama-3-8B's attention geometry
+    (ModelConfig.llama3_8b_shape, heteroserve/config.py:85-93): 32 query heads
+    sharing 8 KV heads, so each KV page serves a group of 4."""
+    torch = _torch()
+    rng = np.random.default_rng(1)
+    return build_decode("C2-gqa", c2_ctx(rng), 32, 8, 128, 65536, dtype or torch.bfloat16,
+                        device, 1, rng=rng)
+
+
 def c3_decode(device, dtype=None) -> PagedCase:
     torch = _torch()
     rng = np.random.default_rng(2)
@@ -266,6 +277,7 @@ def c5_pack_ids(num_blocks: int = C5_POOL_BLOCKS, n: int = 4096) -> list:
 CONFIGS = {
     "C1": c1_decode,
     "C2": c2_decode,
+    "C2-gqa": c2_gqa_decode,
     "C3": c3_decode,
     "C4": c4_prefill,
     "C5-decode": c5_decode,

@@ -21,6 +21,7 @@ builder, which this image does not have.
                   per-sequence forms for configurations too large to pad
     recurrences   online_softmax_reference, split_merge_reference,
                   tiled_prefill_reference, NEG_BIG
-    kvpack        export_blocks, write_blocks, gather_kv_batch
+    kvpack        export_blocks, write_blocks (numpy and torch forms),
+                  gather_kv_batch, KV-row writes, block tables
     splits        choose_num_splits
 """

@@ -29,6 +29,29 @@ def write_blocks(pool: np.ndarray, block_ids, payload: np.ndarray) -> None:
         pool[:, :, blk] = payload[i]
 
 
+def export_blocks_torch(pool, block_ids):
+    """The same payload with torch on a CPU pool tensor, in the reference's
+    own expression: pool[:, :, idx].permute(2, 0, 1, 3, 4, 5).contiguous().
+
+    heteroserve/kv/torch_blocks.py:137-148 (export_blocks_device).  The
+    benchmark times this as the pack's CPU baseline.
+    """
+    import torch
+
+    idx = torch.as_tensor(list(block_ids), dtype=torch.long)
+    return pool[:, :, idx].permute(2, 0, 1, 3, 4, 5).contiguous()
+
+
+def write_blocks_torch(pool, block_ids, payload) -> None:
+    """pool[:, :, blk] = payload[i] for each (i, blk), in order, with torch on
+    CPU tensors: the reference's per-block loop.
+
+    heteroserve/kv/torch_blocks.py:150-154 (write_blocks_device).
+    """
+    for i, blk in enumerate(block_ids):
+        pool[:, :, int(blk)] = payload[i]
+
+
 def gather_kv_batch(pool: np.ndarray, tables, length: int, layer: int):
     """([B, length, H, D], same for V) through each sequence's block list.
 

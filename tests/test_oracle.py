@@ -345,6 +345,30 @@ def test_pack_oracle():
     assert np.array_equal(dst[:, :, 3], payload[1])
 
 
+def test_pack_oracle_torch_forms():
+    """The torch forms the benchmark times as CPU baselines (torch_blocks.py:
+    137-154): the same explicit index loops as the numpy form, and the
+    per-block unpack loop with a repeated id (a later payload entry wins)."""
+    check_pack_by_loops(lambda pool, ids: kvp.export_blocks_torch(torch.from_numpy(pool),
+                                                                  ids).numpy())
+    rng = np.random.default_rng(4)
+    pool = torch.from_numpy(rng.integers(-30000, 30000, size=(2, 2, 9, 4, 3, 6)).astype(np.int16))
+    payload = torch.from_numpy(rng.integers(-30000, 30000, size=(4, 2, 2, 4, 3, 6))
+                               .astype(np.int16))
+    dst = pool.clone()
+    ids = [7, 0, 7, 3]
+    kvp.write_blocks_torch(dst, ids, payload)
+    for blk in range(9):
+        if blk in (0, 3, 7):
+            i = max(j for j, x in enumerate(ids) if x == blk)
+            assert torch.equal(dst[:, :, blk], payload[i]), blk
+        else:
+            assert torch.equal(dst[:, :, blk], pool[:, :, blk]), blk
+    ref = pool.numpy().copy()
+    kvp.write_blocks(ref, ids, payload.numpy())
+    assert np.array_equal(ref, dst.numpy())
+
+
 def test_kv_write_oracle():
     """slots_for, the engine's scatter and write_kv (torch_blocks.py:68-106,
     torch_engine.py:239-240)."""
