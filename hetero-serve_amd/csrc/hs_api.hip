@@ -455,16 +455,18 @@ int hs_kv_scatter(void* k_cache, void* v_cache, int kv_dtype, int64_t num_slots,
 }
 
 int hs_kv_append(void* k_cache, void* v_cache, int kv_dtype, int NB, int BS, int Hkv, int D,
-                 const int32_t* block_tables, int MB, const int32_t* positions,
+                 const int32_t* block_tables, int B, int MB, const int32_t* positions,
                  const int32_t* seq_ids, int64_t n, const void* k_src, const void* v_src,
                  int src_dtype, int64_t src_row_stride, void* stream) {
   const int rc = check_kv_write(k_cache, v_cache, kv_dtype, Hkv, D, n, k_src, v_src, src_dtype,
                                 src_row_stride);
   if (rc != HS_OK) return rc;
-  if (NB <= 0 || BS <= 0 || MB <= 0) return fail(HS_EINVAL, "append sizes must be positive");
+  if (NB <= 0 || BS <= 0 || B <= 0 || MB <= 0)
+    return fail(HS_EINVAL, "append sizes must be positive");
   if (n == 0) return HS_OK;
   if (!block_tables || !positions) return fail(HS_EINVAL, "null pointer");
-  return launch_kv_append(k_cache, v_cache, kv_dtype, NB, BS, (int64_t)Hkv * D, block_tables, MB,
+  return launch_kv_append(k_cache, v_cache, kv_dtype, NB, BS, (int64_t)Hkv * D, block_tables, B,
+                          MB,
                           positions, seq_ids, n, k_src, v_src, src_dtype, src_row_stride,
                           static_cast<hipStream_t>(stream));
 }

@@ -125,7 +125,8 @@ int launch_kv_scatter(void* k_cache, void* v_cache, int kv_dtype, int64_t num_sl
 int launch_block_tables(const int32_t* packed, int B, int width, int32_t* out,
                         hipStream_t stream);
 int launch_kv_append(void* k_cache, void* v_cache, int kv_dtype, int NB, int BS,
-                     int64_t row_elems, const int32_t* bt, int MB, const int32_t* positions,
+                     int64_t row_elems, const int32_t* bt, int B, int MB,
+                     const int32_t* positions,
                      const int32_t* seq_ids, int64_t n, const void* k_src, const void* v_src,
                      int src_dtype, int64_t src_row_stride, hipStream_t stream);
 

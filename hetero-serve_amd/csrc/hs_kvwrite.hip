@@ -128,7 +128,7 @@ struct RowMap {
   const int32_t* positions;    //              [n] absolute positions
   const int32_t* seq_ids;      //              [n] row -> sequence, or null (row i = sequence i)
   int64_t num_slots;           // NB * BS
-  int NB, BS, MB;
+  int NB, BS, B, MB;           // B: table rows; a sequence index must be below it
 
   __device__ int64_t slot(int64_t i) const {
     if (slots) {
@@ -137,7 +137,7 @@ struct RowMap {
     }
     const int64_t b = seq_ids ? seq_ids[i] : i;
     const int pos = positions[i];
-    if (b < 0 || pos < 0 || pos / BS >= MB) return -1;
+    if (b < 0 || b >= B || pos < 0 || pos / BS >= MB) return -1;
     const int blk = bt[b * MB + pos / BS];
     if (blk < 0 || blk >= NB) return -1;
     return (int64_t)blk * BS + pos % BS;
@@ -306,7 +306,8 @@ int launch_kv_scatter(void* k_cache, void* v_cache, int kv_dtype, int64_t num_sl
 }
 
 int launch_kv_append(void* k_cache, void* v_cache, int kv_dtype, int NB, int BS,
-                     int64_t row_elems, const int32_t* bt, int MB, const int32_t* positions,
+                     int64_t row_elems, const int32_t* bt, int B, int MB,
+                     const int32_t* positions,
                      const int32_t* seq_ids, int64_t n, const void* k_src, const void* v_src,
                      int src_dtype, int64_t src_row_stride, hipStream_t stream) {
   RowMap map{};
@@ -316,6 +317,7 @@ int launch_kv_append(void* k_cache, void* v_cache, int kv_dtype, int NB, int BS,
   map.num_slots = (int64_t)NB * BS;
   map.NB = NB;
   map.BS = BS;
+  map.B = B;
   map.MB = MB;
   return launch_kv_write(k_cache, v_cache, kv_dtype, k_src, v_src, src_dtype, src_row_stride,
                          row_elems, n, map, stream);

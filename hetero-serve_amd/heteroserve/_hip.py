@@ -22,7 +22,7 @@ import threading
 from pathlib import Path
 from typing import Optional
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
 
 _lock = threading.Lock()
@@ -63,7 +63,8 @@ _SIGNATURES = {
     "hs_kv_scatter": (_c_int, [_c_vp, _c_vp, _c_int, _c_i64, _c_int, _c_int, _c_vp, _c_i64,
                                _c_vp, _c_vp, _c_int, _c_i64, _c_vp]),
     "hs_kv_append": (_c_int, [_c_vp, _c_vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_vp,
-                              _c_int, _c_vp, _c_vp, _c_i64, _c_vp, _c_vp, _c_int, _c_i64, _c_vp]),
+                              _c_int, _c_int, _c_vp, _c_vp, _c_i64, _c_vp, _c_vp, _c_int, _c_i64,
+                              _c_vp]),
 }
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)
@@ -480,7 +481,7 @@ def kv_append(k_cache, v_cache, block_tables, positions, k, v, seq_ids=None) -> 
         raise RuntimeError("without seq_ids, row i uses table row i: more rows than tables")
     with _DeviceGuard(dev):
         check(L.hs_kv_append(k_cache.data_ptr(), v_cache.data_ptr(), dtype_code(k_cache.dtype), NB,
-                             BS, Hkv, D, bt.data_ptr(), bt.shape[1], pos.data_ptr(),
+                             BS, Hkv, D, bt.data_ptr(), bt.shape[0], bt.shape[1], pos.data_ptr(),
                              None if sid is None else sid.data_ptr(), n, k.data_ptr(),
                              v.data_ptr(), dtype_code(k.dtype), stride, stream_of(dev)))
 

@@ -177,8 +177,9 @@ def append_kv(k_cache, v_cache, block_tables, positions, k, v, seq_ids=None) -> 
     ``seq_ids[i]`` (row i of the tables when None), slots computed on the GPU
     from the int32 ``[B, MB]`` block tables.  Replaces the engine's
     per-sequence slot loop (torch_engine.py:221-227, a device-to-host copy per
-    sequence) and the scatter after it.  Rows whose position is past the
-    table or whose table entry is padding (-1) are not written.
+    sequence) and the scatter after it.  Rows whose sequence id is outside
+    ``[0, B)``, whose position is past the table or whose table entry is
+    padding (-1) are not written.
     """
     _hip.kv_append(k_cache, v_cache, block_tables, positions, k, v, seq_ids)
 

@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define HS_ABI_VERSION 4
+#define HS_ABI_VERSION 5
 
 /* KV element type codes (the pool dtype). */
 #define HS_DTYPE_F32 0
@@ -177,7 +177,11 @@ size_t hs_prefill_workspace_bytes(int B, int max_seqlen_q, int H, int D, int use
  *   use_mfma = 1: paged_attention_prefill_wmma,
  *                 heteroserve/model/paged_attn_wmma.py:256-318
  *                 (fp16 matrix-core operands with fp32 accumulation; KV dtype
- *                 f16 or bf16, BS == 16, D in {32,64,128})
+ *                 f16 or bf16, BS == 16, D in {32,64,128}.  A query tile
+ *                 whose operands fp16 cannot hold -- a bf16 K/V value of
+ *                 magnitude >= 65536, a scaled query >= 65520 -- is
+ *                 recomputed with fp32 arithmetic instead; the same holds
+ *                 for the matrix-core decode paths below)
  *
  *   q   [B, S, H, D] float32;  out [B, S, H, D] float32
  *   workspace  NULL, or device scratch of hs_prefill_workspace_bytes(B, S, H,
@@ -265,8 +269,10 @@ int hs_kv_scatter(void* k_cache, void* v_cache, int kv_dtype, int64_t num_slots,
  * sequence's block table (int32 [B, MB], -1 padded) and its absolute
  * position:  slot = block_tables[s][pos / BS] * BS + pos % BS,  with
  * s = seq_ids[i] (or s = i when seq_ids is NULL) and pos = positions[i].
- * Rows whose position is negative or past the table, or whose table entry is
- * outside [0, NB), are skipped.
+ * Rows whose sequence index is outside [0, B), whose position is negative or
+ * past the table, or whose table entry is outside [0, NB), are skipped: the
+ * kernel reads no table row past B and writes no slot outside the cache.
+ * (Version 5 of the ABI added B.)
  * Replaces: the per-sequence slot loop of decode_batch_paged
  *           (heteroserve/model/torch_engine.py:221-227, one .tolist() per
  *           sequence) followed by the scatter at :239-240; and
@@ -274,7 +280,7 @@ int hs_kv_scatter(void* k_cache, void* v_cache, int kv_dtype, int64_t num_slots,
  *           (heteroserve/kv/torch_blocks.py:68-73, 89-106) for a chunk.
  */
 int hs_kv_append(void* k_cache, void* v_cache, int kv_dtype, int NB, int BS, int Hkv, int D,
-                 const int32_t* block_tables, int MB, const int32_t* positions,
+                 const int32_t* block_tables, int B, int MB, const int32_t* positions,
                  const int32_t* seq_ids, int64_t n, const void* k_src, const void* v_src,
                  int src_dtype, int64_t src_row_stride, void* stream);
 

@@ -40,7 +40,7 @@ def test_header_declarations_are_bound_by_the_loader():
 def test_library_exports_every_declared_symbol(lib):
     for name in _declared_functions():
         assert hasattr(lib, name), name
-    assert lib.hs_abi_version() == 4
+    assert lib.hs_abi_version() == 5
     assert lib.hs_last_error() == b""
 
 
@@ -99,10 +99,13 @@ def test_argument_errors_need_no_device(lib):
     rc = lib.hs_kv_scatter(fake, fake, 2, 128, 4, 64, None, 3, fake, fake, 0, 256, None)
     assert rc == -1 and b"null" in lib.hs_last_error()
     assert lib.hs_kv_scatter(None, None, 2, 128, 4, 64, None, 0, None, None, 0, 256, None) == 0
-    rc = lib.hs_kv_append(fake, fake, 2, 8, 0, 4, 64, fake, 2, fake, None, 3, fake, fake, 0,
+    rc = lib.hs_kv_append(fake, fake, 2, 8, 0, 4, 64, fake, 1, 2, fake, None, 3, fake, fake, 0,
                           256, None)
     assert rc == -1 and b"positive" in lib.hs_last_error()
-    rc = lib.hs_kv_append(fake, fake, 2, 8, 16, 4, 64, None, 2, fake, None, 3, fake, fake, 0,
+    rc = lib.hs_kv_append(fake, fake, 2, 8, 16, 4, 64, fake, 0, 2, fake, None, 3, fake, fake, 0,
+                          256, None)                              # no table rows
+    assert rc == -1 and b"positive" in lib.hs_last_error()
+    rc = lib.hs_kv_append(fake, fake, 2, 8, 16, 4, 64, None, 1, 2, fake, None, 3, fake, fake, 0,
                           256, None)
     assert rc == -1 and b"null" in lib.hs_last_error()
 

@@ -154,6 +154,32 @@ def test_append_prefill_chunk_and_invalid_rows():
     _assert_same(gv, want_v)
 
 
+def test_append_skips_sequence_ids_outside_the_tables():
+    """Rows whose sequence id is negative or >= the number of table rows are
+    skipped: the kernel reads no table row past B (here the row after the
+    table's last holds a valid block id in the same allocation, which a
+    missing bound would follow) and the cache is bit-identical apart from
+    the valid rows."""
+    pk = _pack()
+    nb, bs, h, d = 16, 16, 2, 64
+    big = torch.tensor([[3, 5], [8, 1], [11, 12]], dtype=torch.int32, device=DEV)
+    bt = big[:2]                                   # B = 2 tables; row 2 lies beyond
+    k = _rows(5, h, d, torch.float32, 40, special=False)
+    v = _rows(5, h, d, torch.float32, 41, special=False)
+    seq = torch.tensor([0, 2, 1, -1, 7], dtype=torch.int32, device=DEV)
+    pos = torch.tensor([3, 4, 20, 1, 0], dtype=torch.int32, device=DEV)
+    gen = torch.Generator(device=DEV).manual_seed(42)
+    gk = torch.randn(nb, bs, h, d, generator=gen, device=DEV).to(torch.bfloat16)
+    gv = torch.randn(nb, bs, h, d, generator=gen, device=DEV).to(torch.bfloat16)
+    want_k, want_v = gk.cpu().clone(), gv.cpu().clone()
+    slots = [int(kvp.slots_for([3, 5], [3], bs)[0]), int(kvp.slots_for([8, 1], [20], bs)[0])]
+    kvp.scatter_rows(want_k, slots, k[[0, 2]])
+    kvp.scatter_rows(want_v, slots, v[[0, 2]])
+    pk.append_kv(gk, gv, bt, pos, k.to(DEV), v.to(DEV), seq_ids=seq)
+    _assert_same(gk, want_k)
+    _assert_same(gv, want_v)
+
+
 def test_write_kv_matches_reference_allocator():
     """HipKVMixin.write_kv == TorchBlockAllocator.write_kv (torch_blocks.py:
     89-106) for the tiny model's shape, then read back by the GPU gather."""
