@@ -20,8 +20,13 @@ partitions plus a log-sum-exp merge), which computes the same function.
 Difference from the reference: when the HIP library is unavailable the
 reference silently computes with torch; this module raises RuntimeError
 instead, so a caller can never get a CPU result it did not ask for.  The
-worker only calls it when ``which_backend() == "cuda"`` (worker.py:203-211),
-so its behaviour is unchanged.
+worker calls ``paged_attention`` when ``which_backend() == "cuda"`` and also,
+with no GPU kernel at all, when HETEROSERVE_FORCE_PAGED is set
+(worker.py:209-211; the reference's CPU test test_distributed.py:326-371 runs
+that way).  So the binding that goes into the reference tree keeps the
+reference's own torch branch for that case (the module's
+``paged_attention_torch``, which stays there); this repository ships no CPU
+path.
 """
 
 from __future__ import annotations

@@ -11,7 +11,10 @@ build_error :258, paged_attention_prefill :263-278).
 
 Runs libhsattn's row kernel (one online-softmax pass per query row and head,
 fp32 arithmetic, any KV dtype).  Difference from the reference: no torch
-fallback -- RuntimeError when the library is unavailable.
+fallback -- RuntimeError when the library is unavailable.  The binding that
+goes into the reference tree keeps the reference's torch branch
+(``paged_attention_prefill_torch``) for hosts without the library, which the
+worker reaches under HETEROSERVE_FORCE_PAGED (worker.py:209-211).
 """
 
 from __future__ import annotations
