@@ -289,6 +289,65 @@ int hs_decode(const float* q, const void* k_cache, const void* v_cache, int kv_d
                        workspace_bytes, stream, false);
 }
 
+}  // extern "C"
+
+namespace hs {
+
+// Scratch of hs_decode_noalloc: the decode's partition states live here
+// instead of in a caller workspace.  Each device holds its own copy (the
+// runtime allocates it when it loads this library's code on that device) until
+// the process ends.  In host code `scratch` is only a stand-in symbol; its
+// address on a device comes from hipGetSymbolAddress with that device current.
+static __device__ __align__(256) uint8_t scratch[HS_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+
+// Device address of `scratch` on the current device, looked up once per
+// device and kept.
+static int noalloc_scratch(void** out) {
+  static std::mutex mu;
+  static void* ptr[kMaxDevices];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return fail(HS_EHIP, "hipGetDevice failed");
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(HS_EUNSUPPORTED, "device " + std::to_string(dev) + " out of range");
+  std::lock_guard<std::mutex> lock(mu);
+  if (!ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return fail(HS_EHIP, std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+    ptr[dev] = p;
+  }
+  *out = ptr[dev];
+  return HS_OK;
+}
+
+}  // namespace hs
+
+extern "C" {
+
+int hs_decode_noalloc(const float* q, const void* k_cache, const void* v_cache, int kv_dtype,
+                      int num_blocks, const int32_t* block_tables, const int32_t* context_lens,
+                      float* out, int B, int H, int Hkv, int D, int BS, int MB, float scale,
+                      int num_splits, int partition_tokens, void* stream) {
+  const size_t need = hs_decode_workspace_bytes(B, H, Hkv, D, BS, MB, num_splits,
+                                                partition_tokens);
+  if (need > (size_t)HS_NOALLOC_SCRATCH_BYTES)
+    return fail(HS_EWORKSPACE, "hs_decode_noalloc: this call needs " + std::to_string(need) +
+                                   " bytes of partition state, more than the library's fixed " +
+                                   std::to_string((size_t)HS_NOALLOC_SCRATCH_BYTES) +
+                                   "; use hs_decode with a workspace");
+  void* ws = nullptr;
+  if (need > 0) {
+    const int rc = noalloc_scratch(&ws);
+    if (rc != HS_OK) return rc;
+  }
+  return decode_common(q, k_cache, v_cache, kv_dtype, num_blocks, block_tables, context_lens,
+                       out, B, H, Hkv, D, BS, MB, scale, num_splits, partition_tokens, ws,
+                       need > 0 ? (size_t)HS_NOALLOC_SCRATCH_BYTES : 0, stream, false);
+}
+
 size_t hs_decode_shared_workspace_bytes(int B, int H, int Hkv, int D, int BS, int MB,
                                         int partition_tokens) {
   const size_t base = hs_decode_workspace_bytes(B, H, Hkv, D, BS, MB, 0, partition_tokens);

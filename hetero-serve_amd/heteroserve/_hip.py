@@ -44,6 +44,9 @@ _SIGNATURES = {
     "hs_decode": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_vp, _c_vp, _c_vp,
                            _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float,
                            _c_int, _c_int, _c_vp, _c_size, _c_vp]),
+    "hs_decode_noalloc": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_vp, _c_vp, _c_vp,
+                                   _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float,
+                                   _c_int, _c_int, _c_vp]),
     "hs_decode_shared_workspace_bytes": (_c_size, [_c_int] * 7),
     "hs_decode_shared": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_vp, _c_vp, _c_vp,
                                   _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float,

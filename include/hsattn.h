@@ -128,6 +128,27 @@ int hs_decode(const float* q, const void* k_cache, const void* v_cache, int kv_d
               size_t workspace_bytes, void* stream);
 
 /*
+ * hs_decode without a workspace argument: the partition states go to a
+ * scratch array of HS_NOALLOC_SCRATCH_BYTES (64 MiB) inside the library, one
+ * per device, held until the process ends.  Same arguments and result as
+ * hs_decode (bit for bit: same kernels, same decomposition); a call needing
+ * more than the fixed size (hs_decode_workspace_bytes(...) >
+ * HS_NOALLOC_SCRATCH_BYTES) fails with HS_EWORKSPACE before launching.  It
+ * allocates nothing: no hipMalloc, no hipFree, no allocating library call.
+ * Every call on a device shares that device's scratch, so calls that overlap
+ * in time on one device (two streams, two threads) race and must not be
+ * issued.
+ * No counterpart in the reference.  It is for callers that cannot allocate
+ * device memory: code under HIP graph capture, tight serving loops,
+ * harnesses that forbid allocation.
+ */
+#define HS_NOALLOC_SCRATCH_BYTES (64u << 20)
+int hs_decode_noalloc(const float* q, const void* k_cache, const void* v_cache, int kv_dtype,
+                      int num_blocks, const int32_t* block_tables, const int32_t* context_lens,
+                      float* out, int B, int H, int Hkv, int D, int BS, int MB, float scale,
+                      int num_splits, int partition_tokens, void* stream);
+
+/*
  * Decode for batches whose sequences share pages (prefix caching: the same
  * block ids at the same positions of several block tables).  Computes what
  * hs_decode(num_splits = 0, partition_tokens) computes.  A partition of
