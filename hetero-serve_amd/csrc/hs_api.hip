@@ -101,16 +101,16 @@ struct DecodePlan {
 // tokens, 14.8 at 64, 14.3 at 32, 15.8 at 16 (the merge grows).
 static int default_partition(int B, int H, int Hkv, int BS, int MB) {
   const int G = H / Hkv;
-  int pt = G >= 8 && Hkv * ((G + 31) / 32) <= 2
+  int pt = G >= 8 && (int64_t)Hkv * (((int64_t)G + 31) / 32) <= 2
                ? kDefaultPartition
                : std::min(kDefaultPartition, 1024 / row_attn_heads_per_wave(H, Hkv));
   int dev = 0;
   const int cus = hipGetDevice(&dev) == hipSuccess ? device_cu_count(dev) : 0;
   if (cus <= 0) return pt;
   const int64_t max_ctx = (int64_t)MB * BS;
-  const int64_t waves_per_part = (int64_t)B * Hkv * (G / row_attn_heads_per_wave(H, Hkv));
+  const int64_t waves_per_part = sat_mul(B, Hkv, G / row_attn_heads_per_wave(H, Hkv));
   while (pt > kMinDefaultPartition &&
-         waves_per_part * ((max_ctx + pt - 1) / pt) < 4 * (int64_t)cus)
+         sat_mul(waves_per_part, ceil_div(max_ctx, pt)) < 4 * (int64_t)cus)
     pt /= 2;
   return pt;
 }
@@ -126,18 +126,25 @@ static int plan_decode(int BS, int MB, int num_splits, int partition_tokens, int
   } else {
     const int pt = partition_tokens > 0 ? partition_tokens : default_pt;
     if (pt % 16 != 0) return fail(HS_EINVAL, "partition_tokens must be a multiple of 16");
-    const int64_t P = (max_ctx + pt - 1) / pt;
+    const int64_t P = ceil_div(max_ctx, pt);
+    if (P > 0x7fffffffLL) return fail(HS_EUNSUPPORTED, "too many partitions per row");
     *plan = {P <= 1 ? 0 : 1, pt, 0, (int)(P < 1 ? 1 : P)};
   }
   return HS_OK;
 }
 
-static size_t decode_ws_bytes(int64_t rows, int H, int D, int P) {
+// Partition states: rows * H * P un-normalised outputs of D floats, padded to
+// 256 bytes, then as many (max, sum) pairs.  INT64_MAX when that does not fit.
+static int64_t decode_ws_bytes(int64_t rows, int H, int D, int P) {
   if (P <= 1) return 0;
-  const size_t acc = (size_t)rows * H * P * D * sizeof(float);
-  const size_t acc_aligned = (acc + 255) & ~(size_t)255;
-  return acc_aligned + (size_t)rows * H * P * 2 * sizeof(float);
+  const int64_t states = sat_mul(rows, H, P);
+  const int64_t acc = sat_mul(states, D, (int64_t)sizeof(float));
+  const int64_t acc_aligned = sat_add(acc, 255) & ~(int64_t)255;
+  return sat_add(acc_aligned, sat_mul(states, 2 * (int64_t)sizeof(float)));
 }
+
+// Sizes a query function cannot report (0 means "none needed" there).
+constexpr int64_t kTooLarge = INT64_MAX;
 
 }  // namespace hs
 
@@ -171,9 +178,14 @@ int64_t hs_choose_num_splits(int64_t num_seqs, int64_t num_heads, int64_t max_co
     return -1;
   }
   // paged_attn_v3.py:224-231
-  const int64_t have = num_seqs * num_heads > 1 ? num_seqs * num_heads : 1;
+  if (num_seqs < 0 || num_heads < 0 || max_context < 0) {
+    set_error("sizes must be non-negative");
+    return -1;
+  }
+  const int64_t prod = sat_mul(num_seqs, num_heads);
+  const int64_t have = prod > 1 ? prod : 1;
   const int64_t by_chain = max_context / 32 > 1 ? max_context / 32 : 1;
-  const int64_t fill = ((int64_t)sms * 8 + have - 1) / have;
+  const int64_t fill = ceil_div((int64_t)sms * 8, have);
   const int64_t to_fill = fill > 1 ? fill : 1;
   int64_t s = by_chain > to_fill ? by_chain : to_fill;
   s = s < 64 ? s : 64;
@@ -187,28 +199,31 @@ size_t hs_decode_workspace_bytes(int B, int H, int Hkv, int D, int BS, int MB, i
   if (plan_decode(BS, MB, num_splits, partition_tokens, default_partition(B, H, Hkv, BS, MB),
                   &plan) != HS_OK)
     return 0;
-  return decode_ws_bytes(B, H, D, plan.P);
+  const int64_t need = decode_ws_bytes(B, H, D, plan.P);
+  return need == kTooLarge ? 0 : (size_t)need;
 }
 
 }  // extern "C"
 
 namespace hs {
 
-static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
-
 // Shared-page plan arrays after the decode workspace: skip [B * P] bytes,
-// members [P * B] int32, units [P * U] int4, unit counts [P] int32.
+// members [P * B] int32, units [P * U] int4, unit counts [P] int32.  `end` is
+// kTooLarge when the sizes do not fit.
 struct ShareLayout {
-  size_t skip, members, units, n_units, end;
+  int64_t skip, members, units, n_units, end;
 };
 
-static ShareLayout share_layout(size_t base, int B, int P, int U) {
+static int64_t align256s(int64_t x) { return sat_add(x, 255) & ~(int64_t)255; }
+
+static ShareLayout share_layout(int64_t base, int B, int P, int64_t U) {
   ShareLayout l;
-  l.skip = align256(base);
-  l.members = align256(l.skip + (size_t)B * P);
-  l.units = align256(l.members + (size_t)P * B * sizeof(int32_t));
-  l.n_units = align256(l.units + (size_t)P * U * 4 * sizeof(int32_t));
-  l.end = l.n_units + (size_t)P * sizeof(int32_t);
+  l.skip = align256s(base);
+  l.members = align256s(sat_add(l.skip, sat_mul(B, P)));
+  l.units = align256s(sat_add(l.members, sat_mul(P, B, (int64_t)sizeof(int32_t))));
+  l.n_units = align256s(sat_add(l.units, sat_mul(P, U, 4 * (int64_t)sizeof(int32_t))));
+  l.end = sat_add(l.n_units, sat_mul(P, (int64_t)sizeof(int32_t)));
+  if (l.end >= kTooLarge - 255) l.end = kTooLarge;
   return l;
 }
 
@@ -229,7 +244,10 @@ static int decode_common(const float* q, const void* k_cache, const void* v_cach
   if ((rc = plan_decode(BS, MB, num_splits, partition_tokens, default_partition(B, H, Hkv, BS, MB),
                         &plan)) != HS_OK)
     return rc;
-  const size_t need = decode_ws_bytes(B, H, D, plan.P);
+  const int64_t need_i = decode_ws_bytes(B, H, D, plan.P);
+  if (need_i == kTooLarge)
+    return fail(HS_EUNSUPPORTED, "decode partition states too large for these sizes");
+  const size_t need = (size_t)need_i;
   if (need > 0 && (!workspace || workspace_bytes < need))
     return fail(HS_EWORKSPACE, "decode needs " + std::to_string(need) + " workspace bytes, got " +
                                    std::to_string(workspace ? workspace_bytes : 0));
@@ -261,9 +279,10 @@ static int decode_common(const float* q, const void* k_cache, const void* v_cach
   if (!shared_pages || !shared_pages_apply(a, kv_dtype, D)) return launch_row_attn(a, kv_dtype, D, st);
   SharePlanArgs sp{};
   sp.per_unit = share_per_unit(H, Hkv);
-  sp.U = share_unit_slots(B, sp.per_unit);
-  const ShareLayout l = share_layout(need, B, plan.P, sp.U);
-  if (workspace_bytes < l.end)
+  sp.U = (int)share_unit_slots(B, sp.per_unit);   // B <= 2048 here (shared_pages_apply)
+  const ShareLayout l = share_layout((int64_t)need, B, plan.P, sp.U);
+  if (l.end == kTooLarge) return fail(HS_EUNSUPPORTED, "shared-page plan too large");
+  if (workspace_bytes < (size_t)l.end)
     return fail(HS_EWORKSPACE, "shared-page decode needs " + std::to_string(l.end) +
                                    " workspace bytes, got " + std::to_string(workspace_bytes));
   char* ws = static_cast<char*>(workspace);
@@ -357,7 +376,9 @@ size_t hs_decode_shared_workspace_bytes(int B, int H, int Hkv, int D, int BS, in
       HS_OK)
     return 0;
   const int pu = H / Hkv <= 32 ? share_per_unit(H, Hkv) : 1;
-  return share_layout(base, B, plan.P, share_unit_slots(B, pu > 0 ? pu : 1)).end;
+  const int64_t end = share_layout((int64_t)base, B, plan.P,
+                                   share_unit_slots(B, pu > 0 ? pu : 1)).end;
+  return end == kTooLarge ? 0 : (size_t)end;
 }
 
 int hs_decode_shared(const float* q, const void* k_cache, const void* v_cache, int kv_dtype,
@@ -451,7 +472,8 @@ size_t hs_prefill_workspace_bytes(int B, int max_seqlen_q, int H, int D, int use
   const int cus = device_cu_count(dev);
   if (cus <= 0) return 0;
   const PrefillPlan plan = plan_prefill_mfma(B, max_seqlen_q, H, D, cus, true);
-  return prefill_workspace_bytes(plan, B, max_seqlen_q, H, D);
+  const int64_t need = prefill_workspace_bytes(plan, B, max_seqlen_q, H, D);
+  return need == INT64_MAX ? 0 : (size_t)need;
 }
 
 int hs_kv_pack(const void* pool, int L, int NB, int64_t page_bytes, const int64_t* block_ids,

@@ -135,6 +135,31 @@ __device__ inline int64_t safe_block(int32_t blk, int num_blocks) {
 }
 
 // ---------------------------------------------------------------------------
+// Host-side size arithmetic: a product or sum of non-negative sizes that would
+// overflow int64_t saturates to INT64_MAX, so the caller's "too large" check
+// rejects it instead of wrapping (signed overflow is undefined in C++).
+// ---------------------------------------------------------------------------
+
+inline int64_t sat_mul(int64_t a, int64_t b) {
+  int64_t r;
+  return __builtin_mul_overflow(a, b, &r) ? INT64_MAX : r;
+}
+
+inline int64_t sat_add(int64_t a, int64_t b) {
+  int64_t r;
+  return __builtin_add_overflow(a, b, &r) ? INT64_MAX : r;
+}
+
+inline int64_t sat_mul(int64_t a, int64_t b, int64_t c) { return sat_mul(sat_mul(a, b), c); }
+
+inline int64_t sat_mul(int64_t a, int64_t b, int64_t c, int64_t d) {
+  return sat_mul(sat_mul(a, b), sat_mul(c, d));
+}
+
+// ceil(a / b) for a >= 0, b > 0, without forming a + b - 1
+inline int64_t ceil_div(int64_t a, int64_t b) { return a / b + (a % b != 0); }
+
+// ---------------------------------------------------------------------------
 // Host-side error reporting (thread-local, read back by hs_last_error)
 // ---------------------------------------------------------------------------
 

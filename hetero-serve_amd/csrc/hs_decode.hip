@@ -173,7 +173,7 @@ static void launch_merge(const RowAttnArgs& a, int D, hipStream_t stream) {
 template <typename T, int D, int G>
 static void launch_part(const RowAttnArgs& a, hipStream_t stream) {
   const int tpl = 64 / (D / Elem<T>::kVec);
-  const int64_t gx = (int64_t)a.rows * a.P * ((a.H / G + kDecodeWaves - 1) / kDecodeWaves);
+  const int64_t gx = sat_mul(a.rows, a.P, ceil_div(a.H / G, kDecodeWaves));   // checked by the caller
   const dim3 grid((unsigned)gx), block(kDecodeWaves * 64);
   if (a.BS % tpl == 0)
     hipLaunchKernelGGL((row_attn_part_kernel<T, D, true, G>), grid, block, 0, stream, a);
@@ -220,7 +220,7 @@ int launch_row_attn(const RowAttnArgs& a, int kv_dtype, int D, hipStream_t strea
     gx = gqa_mfma_grid(a);
   } else {
     const int G = row_attn_heads_per_wave(a.H, a.Hkv);
-    gx = (int64_t)a.rows * a.P * ((a.H / G + kDecodeWaves - 1) / kDecodeWaves);
+    gx = sat_mul(a.rows, a.P, ceil_div(a.H / G, kDecodeWaves));
   }
   if (gx <= 0) return HS_OK;
   if (gx > 0x7fffffffLL)

@@ -368,8 +368,8 @@ void gqa_mfma_part_kernel(RowAttnArgs a) {
 
 int64_t grid_size(const RowAttnArgs& a) {
   const int G = a.H / a.Hkv;
-  const int64_t waves = (int64_t)a.rows * a.P * a.Hkv * ((G + kHeadsPerWave - 1) / kHeadsPerWave);
-  return (waves + kGqaWaves - 1) / kGqaWaves;
+  const int64_t waves = sat_mul(a.rows, a.P, a.Hkv, ceil_div(G, kHeadsPerWave));
+  return ceil_div(waves, kGqaWaves);
 }
 
 template <typename T, int D>
@@ -681,8 +681,8 @@ bool shared_pages_apply(const RowAttnArgs& a, int kv_dtype, int D) {
          a.S == 1;
 }
 
-int share_unit_slots(int B, int per_unit) {
-  return (B + kShareMin - 1) / kShareMin + (B + per_unit - 1) / per_unit;
+int64_t share_unit_slots(int B, int per_unit) {
+  return ceil_div(B, kShareMin) + ceil_div(B, per_unit);
 }
 
 void launch_share_plan(const RowAttnArgs& a, const SharePlanArgs& s, hipStream_t stream) {

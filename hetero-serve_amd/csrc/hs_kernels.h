@@ -91,7 +91,7 @@ struct SharePlanArgs {
   int per_unit;        // sequences per unit (32 query slots / G heads per KV head)
 };
 bool shared_pages_apply(const RowAttnArgs& a, int kv_dtype, int D);
-int share_unit_slots(int B, int per_unit);
+int64_t share_unit_slots(int B, int per_unit);
 void launch_share_plan(const RowAttnArgs& a, const SharePlanArgs& s, hipStream_t stream);
 void launch_shared_pages(const RowAttnArgs& a, const SharePlanArgs& s, int kv_dtype, int D,
                          hipStream_t stream);
@@ -145,6 +145,6 @@ struct PrefillPlan {
   int n_split;   // key-range parts per query tile (1: none)
 };
 PrefillPlan plan_prefill_mfma(int B, int max_rows, int H, int D, int cus, bool can_split);
-size_t prefill_workspace_bytes(const PrefillPlan& p, int B, int max_rows, int H, int D);
+int64_t prefill_workspace_bytes(const PrefillPlan& p, int B, int max_rows, int H, int D);
 
 }  // namespace hs

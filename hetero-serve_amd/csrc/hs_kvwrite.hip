@@ -243,13 +243,16 @@ int launch_kv_write(void* k_cache, void* v_cache, int kv_dtype, const void* k_sr
                     int64_t n, const RowMap& map, hipStream_t stream) {
   if (n == 0) return HS_OK;
   const int64_t sb = dtype_bytes(src_dtype), cb = dtype_bytes(kv_dtype);
-  const int64_t stride_bytes = src_row_stride * sb;
+  const int64_t stride_bytes = sat_mul(src_row_stride, sb);
+  if (stride_bytes == INT64_MAX || sat_mul(n, stride_bytes) == INT64_MAX ||
+      sat_mul(map.num_slots, row_elems, cb) == INT64_MAX)
+    return fail(HS_EUNSUPPORTED, "KV write sizes too large for 64-bit offsets");
   // the vector kernels need 16-byte aligned 8-element groups on both sides
   const bool vec = row_elems % 8 == 0 && aligned16(k_src) && aligned16(v_src) &&
                    aligned16(k_cache) && aligned16(v_cache) && stride_bytes % 16 == 0 &&
                    (row_elems * cb) % 16 == 0;
-  const int64_t work = n * row_elems;
-  if ((work + kWriteThreads - 1) / kWriteThreads > 0x7fffffffLL)
+  const int64_t work = sat_mul(n, row_elems);
+  if (ceil_div(work, kWriteThreads) > 0x7fffffffLL)
     return fail(HS_EUNSUPPORTED, "KV write too large for one launch");
   auto* kc = static_cast<uint8_t*>(k_cache);
   auto* vc = static_cast<uint8_t*>(v_cache);
@@ -285,9 +288,9 @@ __global__ __launch_bounds__(kWriteThreads) void block_tables_kernel(const int32
 
 int launch_block_tables(const int32_t* packed, int B, int width, int32_t* out,
                         hipStream_t stream) {
-  const int64_t work = (int64_t)B * width;
+  const int64_t work = (int64_t)B * width;   // both are int: no overflow
   if (work == 0) return HS_OK;
-  if ((work + kWriteThreads - 1) / kWriteThreads > 0x7fffffffLL)
+  if (ceil_div(work, kWriteThreads) > 0x7fffffffLL)
     return fail(HS_EUNSUPPORTED, "block table too large for one launch");
   hipLaunchKernelGGL(block_tables_kernel, dim3((unsigned)((work + kWriteThreads - 1) / kWriteThreads)),
                      dim3(kWriteThreads), 0, stream, packed, B, width, out);

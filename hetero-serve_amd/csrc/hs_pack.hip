@@ -87,10 +87,12 @@ static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 
 int launch_page_copy(const void* pool, void* buf, bool unpack, int L, int NB,
                      int64_t page_bytes, const int64_t* ids, int n, hipStream_t stream) {
-  const int64_t pieces = (page_bytes + kCopyPiece - 1) / kCopyPiece;
-  const int64_t grid = (int64_t)n * L * 2 * pieces;
+  const int64_t pieces = ceil_div(page_bytes, kCopyPiece);
+  const int64_t grid = sat_mul(n, L, 2, pieces);
   if (grid == 0) return HS_OK;
   if (grid > 0x7fffffffLL) return fail(HS_EUNSUPPORTED, "pack grid too large");
+  if (sat_mul(L, 2, NB, page_bytes) == INT64_MAX)
+    return fail(HS_EUNSUPPORTED, "pool too large for 64-bit offsets");
   const bool vec = page_bytes % 16 == 0 && aligned16(pool) && aligned16(buf);
   const uint8_t* pool_b = static_cast<const uint8_t*>(pool);
   uint8_t* buf_b = static_cast<uint8_t*>(buf);
@@ -119,8 +121,8 @@ int launch_page_copy(const void* pool, void* buf, bool unpack, int L, int NB,
 
 int launch_gather_rows(const void* cache, int NB, int BS, int64_t row_bytes, const int32_t* bt,
                        int MB, int B, int length, void* out, hipStream_t stream) {
-  const int64_t pieces = (row_bytes + kCopyPiece - 1) / kCopyPiece;
-  const int64_t grid = (int64_t)B * length * pieces;
+  const int64_t pieces = ceil_div(row_bytes, kCopyPiece);
+  const int64_t grid = sat_mul(B, length, pieces);
   if (grid == 0) return HS_OK;
   if (grid > 0x7fffffffLL) return fail(HS_EUNSUPPORTED, "gather grid too large");
   const bool vec = row_bytes % 16 == 0 && aligned16(cache) && aligned16(out);

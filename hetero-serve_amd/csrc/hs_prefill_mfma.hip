@@ -750,17 +750,18 @@ int launch_typed(PrefillArgs a, int max_rows_per_seq, hipStream_t stream) {
   const int64_t pairs = (int64_t)a.B * a.H;
   a.ranked = a.B <= kMaxRanked;
   if (a.n_split > 1 && !a.ranked) return fail(HS_EUNSUPPORTED, "split prefill needs ranked tiles");
-  const int64_t slots =
-      a.ranked ? (int64_t)a.B * a.n_qt * ((a.H + kXcds - 1) / kXcds) * a.n_split
-               : (pairs + kXcds - 1) / kXcds * a.n_qt;
-  if (slots * kXcds > 0x7fffffffLL) return fail(HS_EUNSUPPORTED, "prefill grid too large");
+  const int64_t slots = a.ranked ? sat_mul(a.B, a.n_qt, ceil_div(a.H, kXcds), a.n_split)
+                                 : sat_mul(ceil_div(pairs, kXcds), a.n_qt);
+  if (sat_mul(slots, kXcds) > 0x7fffffffLL) return fail(HS_EUNSUPPORTED, "prefill grid too large");
   a.slots_per_xcd = (int)slots;
   const dim3 grid((unsigned)(kXcds * a.slots_per_xcd)), block(Shape<D, W>::kThreads);
   hipLaunchKernelGGL((prefill_mfma_kernel<T, D, W>), grid, block, 0, stream, a);
   if (a.n_split > 1) {
-    const int64_t threads = (int64_t)a.B * a.rows_cap * a.H * (D / 4);
-    hipLaunchKernelGGL((prefill_merge_kernel<D>), dim3((unsigned)((threads + 255) / 256)),
-                       dim3(256), 0, stream, a);
+    // the workspace of B * rows_cap * H * (D + 2) floats per part exists, so
+    // this product fits; the grid must still fit one launch
+    const int64_t groups = ceil_div(sat_mul(a.B, a.rows_cap, a.H, D / 4), 256);
+    if (groups > 0x7fffffffLL) return fail(HS_EUNSUPPORTED, "prefill merge grid too large");
+    hipLaunchKernelGGL((prefill_merge_kernel<D>), dim3((unsigned)groups), dim3(256), 0, stream, a);
   }
   return HS_OK;
 }
@@ -790,7 +791,7 @@ int launch_dim(const PrefillArgs& a, int D, bool wide, int max_rows_per_seq, hip
 // 128-row workgroups, which run one wave per SIMD but reach twice as many CUs.
 PrefillPlan plan_prefill_mfma(int B, int max_rows, int H, int D, int cus, bool can_split) {
   const int bm = D >= 64 ? 256 : 128;
-  const int64_t tiles = (int64_t)B * ((max_rows + bm - 1) / bm) * H;
+  const int64_t tiles = sat_mul(B, ceil_div(max_rows, bm), H);
   PrefillPlan p{true, 1};
   if (tiles >= cus) return p;
   const int64_t splits = std::min<int64_t>(kMaxSplit, tiles > 0 ? cus / tiles : 1);
@@ -799,11 +800,12 @@ PrefillPlan plan_prefill_mfma(int B, int max_rows, int H, int D, int cus, bool c
   return p;
 }
 
-size_t prefill_workspace_bytes(const PrefillPlan& p, int B, int max_rows, int H, int D) {
+// INT64_MAX when the sizes do not fit
+int64_t prefill_workspace_bytes(const PrefillPlan& p, int B, int max_rows, int H, int D) {
   if (p.n_split < 2) return 0;
-  const size_t pairs = (size_t)p.n_split * B * max_rows * H;
-  const size_t o_bytes = (pairs * D * sizeof(float) + 255) / 256 * 256;
-  return o_bytes + pairs * sizeof(float2);
+  const int64_t pairs = sat_mul(p.n_split, B, max_rows, H);
+  const int64_t o_bytes = sat_add(sat_mul(pairs, D, (int64_t)sizeof(float)), 255) / 256 * 256;
+  return sat_add(o_bytes, sat_mul(pairs, (int64_t)sizeof(float2)));
 }
 
 int launch_prefill_mfma(const float* q, const int32_t* cu_q, int S, int max_rows_per_seq,
@@ -835,7 +837,9 @@ int launch_prefill_mfma(const float* q, const int32_t* cu_q, int S, int max_rows
   a.n_split = plan.n_split;
   a.rows_cap = max_rows_per_seq;
   if (plan.n_split > 1) {
-    const size_t need = prefill_workspace_bytes(plan, B, max_rows_per_seq, H, D);
+    const int64_t need_i = prefill_workspace_bytes(plan, B, max_rows_per_seq, H, D);
+    if (need_i == INT64_MAX) return fail(HS_EUNSUPPORTED, "prefill split too large");
+    const size_t need = (size_t)need_i;
     if (workspace_bytes < need)
       return fail(HS_EWORKSPACE, "prefill workspace too small: " + std::to_string(need) +
                                      " bytes needed");

@@ -110,6 +110,37 @@ def test_argument_errors_need_no_device(lib):
     assert rc == -1 and b"null" in lib.hs_last_error()
 
 
+def test_extreme_sizes_are_refused_not_wrapped(lib):
+    """Sizes near the int limits: the size queries return 0 (cannot serve)
+    rather than a wrapped value, and the entry points fail with a reason before
+    touching the device.  tests/test_sanitized_abi.py runs this under UBSan,
+    which aborts on any signed overflow in the size and grid arithmetic."""
+    M = 2 ** 31 - 1
+    fake = ctypes.c_void_p(0x1000)
+    assert lib.hs_decode_workspace_bytes(M, M, 1, 256, 16, M, 0, 16) == 0
+    assert lib.hs_decode_workspace_bytes(M, 32, 32, 128, 16, M, 0, 0) == 0
+    assert lib.hs_decode_workspace_bytes(M, M, M, 256, M, M, 0, 0) == 0
+    # large but representable: reported exactly (P = 64 splits, (D + 2) floats)
+    assert lib.hs_decode_workspace_bytes(M, 64, 1, 128, 16, M, 64, 0) == M * 64 * 64 * 520
+    assert lib.hs_decode_shared_workspace_bytes(M, 32, 32, 128, 16, M, 0) == 0
+    assert lib.hs_prefill_workspace_bytes(M, M, M, 128, 1) == 0
+    rc = lib.hs_decode(fake, fake, fake, 2, 8, fake, fake, fake, M, 32, 32, 128, 16, M, 0.1,
+                       0, 0, fake, 2 ** 62, None)
+    assert rc == -2 and b"too large" in lib.hs_last_error()
+    rc = lib.hs_decode_noalloc(fake, fake, fake, 2, 8, fake, fake, fake, M, 32, 32, 128, 16, M,
+                               0.1, 0, 0, None)
+    assert rc == -2 and b"too large" in lib.hs_last_error()
+    rc = lib.hs_prefill(fake, fake, fake, 2, 8, fake, fake, fake, M, M, 4, 4, 64, 16, 2, 0.1,
+                        1, None, 0, None)
+    assert rc == -1 and b"too large" in lib.hs_last_error()
+    rc = lib.hs_kv_pack(fake, M, M, 2 ** 62, fake, M, fake, None)
+    assert rc == -2 and b"too large" in lib.hs_last_error()
+    rc = lib.hs_kv_gather(fake, 8, 16, 2 ** 62, fake, M, M, M, fake, None)
+    assert rc == -2 and b"too large" in lib.hs_last_error()
+    rc = lib.hs_kv_scatter(fake, fake, 2, 2 ** 62, 4, 64, fake, 3, fake, fake, 0, 2 ** 62, None)
+    assert rc == -2 and b"too large" in lib.hs_last_error()
+
+
 def test_workspace_size_formula(lib):
     """hs_decode's workspace: (rows * H * P * D) floats, padded to 256 bytes,
     then rows * H * P (max, sum) pairs; P = ceil(MB * BS / partition).  The
