@@ -214,9 +214,12 @@ static int launch_dim(const RowAttnArgs& a, int D, hipStream_t stream) {
 // waited for whole CUs to drain and finished last.
 int launch_row_attn(const RowAttnArgs& a, int kv_dtype, int D, hipStream_t stream,
                     const SharePlanArgs* shared) {
-  const bool mfma = gqa_mfma_applies(a, kv_dtype, D);
+  const bool bf16mm = bf16mm_applies(a, kv_dtype, D);
+  const bool mfma = !bf16mm && gqa_mfma_applies(a, kv_dtype, D);
   int64_t gx;
-  if (mfma) {
+  if (bf16mm) {
+    gx = bf16mm_grid(a);
+  } else if (mfma) {
     gx = gqa_mfma_grid(a);
   } else {
     const int G = row_attn_heads_per_wave(a.H, a.Hkv);
@@ -234,7 +237,11 @@ int launch_row_attn(const RowAttnArgs& a, int kv_dtype, int D, hipStream_t strea
   }
 
   int rc = HS_OK;
-  if (mfma) {
+  if (bf16mm) {
+    profile_begin(stream);
+    launch_bf16mm_part(a, D, stream);
+    profile_end(stream);
+  } else if (mfma) {
     profile_begin(stream);
     launch_gqa_mfma_part(a, kv_dtype, D, stream);
     profile_end(stream);

@@ -1,0 +1,407 @@
+// Grouped-query decode for bf16 caches on gfx950 matrix cores, at fp32 accuracy.
+//
+// Reference: paged_attn_v2.py:75-157 (one query row per head, KV head
+// h / (H / Hkv), online softmax) and paged_attn_v3.py:75-208 (partitions
+// merged by log-sum-exp).  Same function as the VALU decode kernel
+// (hs_decode.hip); this one serves bf16 caches when two or more query heads
+// share a KV head.
+//
+// Why matrix cores here.  With G query heads per KV head, the VALU kernel's
+// per-token work grows with G (G dot products and G softmax states per
+// 16-byte load) while the bytes read stay the same; at G = 4 it is bound by
+// that arithmetic, not by HBM.  On the matrix cores the G dot products of a
+// token are one column block of an MFMA, and the kernel does a few VALU
+// instructions per page instead.  Measured on MI355X, C2's batch and contexts
+// with 32 query heads (whole decode call, bf16, D = 128): 2 / 4 / 8 / 16 / 32
+// heads per KV head 226 / 130 / 83 / 55 / 57 us, against 232 / 148 us for
+// the VALU kernel and 125 / 95 / 64 us for the fp16 matrix-core kernel
+// (hs_decode_gqa.hip), which bf16 caches no longer use.
+//
+// Numerics.  The cache is bf16, so K and V go to the MFMAs as they are stored
+// (no conversion, no range limit).  The query and the probabilities are fp32;
+// each is split into two bf16 terms, x = hi + lo with hi = bf16(x) and
+// lo = bf16(x - hi), and every product is taken against both terms (as two
+// MFMA columns for up to 8 heads per KV head, as two products above that).
+// hi + lo carries 16 significant bits, the products of bf16 values are exact
+// in the fp32 accumulators, so the result matches fp32 arithmetic to about
+// 2^-16 relative (the reference's kernels compute in fp32).
+//
+// Work decomposition.  One wave serves up to 16 query heads of one KV head
+// for one (row, partition) and walks the partition one 16-token page at a
+// time:
+//   S^T = K . Q^T    v_mfma_f32_16x16x32_bf16, K (16 tokens x 32 dims, from
+//                    LDS) the A operand, Q^T (heads) the B operand, held in
+//                    registers as hi and lo; D / 32 k-steps, two products each
+//   O^T += V^T . P^T v_mfma_f32_16x16x16_bf16, V^T (16 dims x 16 tokens, read
+//                    transposed from the token-major LDS copy by
+//                    ds_read_b64_tr_b16) the A operand, P^T the B operand.  The S^T
+//                    accumulator gives lane l the tokens 4(l/16) + i of head
+//                    l % 16, which is exactly the B-operand layout of the
+//                    second product, so probabilities never leave registers;
+//                    and O^T has head l % 16 in lane l too, so the online
+//                    rescale and the final normalisation are per-lane scalars.
+// Pages are loaded coalesced (D / 8 lanes per head row of one token, 16 bytes
+// each) into registers one page ahead of the one being computed, then
+// written to the wave's own LDS token-major as they came (bf16 needs no
+// conversion).  No barriers: each wave owns its LDS and its LDS operations
+// complete in order.
+//
+// Workgroups are single waves.  The hardware deals workgroups to the eight
+// XCDs round-robin by workgroup id, and the waves are numbered unit-fastest,
+// so the KV heads of one (row, partition) land on different XCDs and every
+// XCD gets an equal share of each row.  With four-wave workgroups on
+// neighbouring KV heads, the XCD a unit ran on depended on the partition
+// index, and the early partitions (live in every row) piled up on a few XCDs
+// (measured on MI355X: 160 -> 138 us on C2's geometry with 8 KV heads).
+//
+// The partition states (m, l, un-normalised acc) have the VALU kernel's
+// layout and meaning, and the same merge kernel combines them; they are
+// written through the wave's LDS so each head's D floats go out as whole
+// 128-byte lines.
+#include "hs_kernels.h"
+
+namespace hs {
+
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef short short4x __attribute__((ext_vector_type(4)));
+typedef float float4x __attribute__((ext_vector_type(4)));
+
+constexpr int kSlots = 16;         // query heads per wave (MFMA N)
+constexpr int kPage = 16;          // tokens per page (block_size)
+constexpr float kSlack = 8.0f;     // lazy-rescale slack, log2 units
+constexpr int kMaxPages = 64;      // pages of a partition: one block id per lane
+
+// One page of K and of V, both token-major as in the cache.  Row paddings:
+// K rows are read as 16-byte MFMA fragments (row j by lane j), V rows by the
+// transposing read below (four rows by each group of 16 lanes); the pads make
+// both conflict-free at D = 128 and keep the 16-byte row stores whole.
+template <int D>
+struct PageLds {
+  static constexpr int kKRow = D + 8;
+  static constexpr int kVRow = D + 16;
+  alignas(16) uint16_t k[kPage][kKRow];
+  alignas(16) uint16_t v[kPage][kVRow];
+};
+
+// V^T fragment of the 16x16x16 product for dims 16 dt .. 16 dt + 15: lane
+// (j, g) gets V[4 g + e][16 dt + j], e = 0..3.  ds_read_b64_tr_b16 transposes
+// within each group of 16 lanes: lane i supplies 8 bytes of row i / 4 of a
+// 4 x 16 block and receives column i (lane layout checked on gfx950).
+template <int D>
+__device__ inline short4x read_vt(const PageLds<D>& w, int dt, int j, int g) {
+  typedef __attribute__((address_space(3))) short4x lds_short4x;
+  const uint16_t* p = &w.v[4 * g + (j >> 2)][16 * dt + 4 * (j & 3)];
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_short4x*)((__attribute__((address_space(3))) void*)(uintptr_t)p));
+}
+
+// x = hi + lo with hi, lo bf16 (RNE); returns the bf16 bit patterns.
+__device__ inline void split_bf16(float x, uint16_t& hi, uint16_t& lo) {
+  const __bf16 h = (__bf16)x;
+  hi = __builtin_bit_cast(uint16_t, h);
+  lo = __builtin_bit_cast(uint16_t, (__bf16)(x - (float)h));
+}
+
+// Both values of x across lanes l and l ^ 16, and across l and l ^ 32.
+__device__ inline float max_across_groups(float x) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+__device__ inline float sum_across_groups(float x) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+template <int D>
+struct PageWalk {
+  static constexpr int kDC = D / 8;           // 16-byte chunks per head row
+  static constexpr int kTpi = 64 / kDC;       // tokens per wave-wide load
+  static constexpr int kLi = kPage / kTpi;    // loads per page, for K and for V
+  static constexpr int kKS = D / 32;          // QK k-steps
+  static constexpr int kDT = D / 16;          // O^T dim tiles
+  static_assert(kLi >= 1 && kTpi * kLi == kPage, "head_dim");
+
+  struct Regs {
+    uint4 k[kLi];    // K load u: token kTpi * u + slot, chunk ck
+    uint4 v[kLi];    // V load u: the same token and chunk
+  };
+};
+
+// One wave's pass over keys [lo, hi) (lo a multiple of 16) of block-table row
+// `bt`, for query slots j < gc whose queries start at element q_off of a.q
+// (slot j at q_off + j * D).  Returns the state in o / m / l: lane l holds
+// column l % 16, dims 16 * dt + 4 * (l / 16) + i of o[dt][i]; m is the running
+// max (log2 units), l this lane's share of the sum (tokens 4 * (l / 16) + i
+// of every page); the caller reduces l across the four lane groups.
+//
+// kCols (gc <= 8): the hi and lo terms are separate MFMA columns instead of
+// separate products: column c < 8 carries the hi term of head c, column
+// c + 8 its lo term, so each product is taken once.  A score is the sum of
+// its two columns (lanes j and j ^ 8, one DPP rotate); both lanes then hold
+// the same score and softmax state, lane j < 8 feeds the hi term of the
+// probability and lane j + 8 the lo term, and o of head c is the sum of
+// columns c and c + 8 (added by the caller).  Without kCols, column j is head
+// j and every product is taken twice, against hi and against lo.
+template <int D, bool kCols>
+__device__ inline void page_walk(const RowAttnArgs& a, PageLds<D>& w, int kvh, int gc,
+                                 const int32_t* bt, int lo, int hi, int64_t q_off,
+                                 float4x (&o)[D / 16], float& m, float& l) {
+  using W = PageWalk<D>;
+  constexpr int kDC = W::kDC, kTpi = W::kTpi, kLi = W::kLi, kKS = W::kKS, kDT = W::kDT;
+  constexpr int kQS = kCols ? 1 : 2;               // products per page and operand
+  const int lane = threadIdx.x & 63;
+  const int j = lane & 15;          // MFMA column of this lane
+  const int g = lane >> 4;          // lane group: tokens 4g .. 4g + 3 of a page
+  const int hj = kCols ? (j & 7) : j;   // query slot (head) of column j
+  const bool lo_col = kCols && j >= 8;
+  const int ck = lane % kDC;        // loads: chunk of the head row
+  const int slot = lane / kDC;      // loads: token slot
+
+  // Block ids of the partition's pages: lane i holds page lo / 16 + i.
+  const int page0 = lo / kPage;
+  const int npages = (hi - lo + kPage - 1) / kPage;
+  const int idv = bt[min(page0 + lane, a.MB - 1)];
+
+  // Q^T fragments, split: lane l holds column j's dims 32 st + 8 g .. + 7.
+  bf16x8 qf[kQS][kKS];
+  {
+    const float sc = hj < gc ? a.qscale : 0.0f;
+    const float* qp = a.q + q_off + (int64_t)min(hj, gc - 1) * D + 8 * g;
+#pragma unroll
+    for (int st = 0; st < kKS; ++st) {
+      const float4 x0 = *reinterpret_cast<const float4*>(qp + 32 * st);
+      const float4 x1 = *reinterpret_cast<const float4*>(qp + 32 * st + 4);
+      const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float x = xs[e] * sc;
+        const __bf16 h = (__bf16)x;
+        const __bf16 r = (__bf16)(x - (float)h);
+        if constexpr (kCols) {
+          qf[0][st][e] = lo_col ? r : h;
+        } else {
+          qf[0][st][e] = h;
+          qf[1][st][e] = r;
+        }
+      }
+    }
+    // Keep the split query in registers: without this anchor the compiler
+    // re-loads and re-splits it on every page to save registers.
+#pragma unroll
+    for (int q = 0; q < kQS; ++q)
+#pragma unroll
+      for (int st = 0; st < kKS; ++st) {
+        uint4& u = reinterpret_cast<uint4&>(qf[q][st]);
+        asm volatile("" : "+v"(u.x), "+v"(u.y), "+v"(u.z), "+v"(u.w));
+      }
+  }
+
+  const int64_t tok = (int64_t)a.Hkv * D;          // elements between tokens of a page
+  // Page addresses: a wave-uniform base (scalar registers) plus one 32-bit
+  // lane offset shared by all loads of a page.
+  const uint16_t* kbase = reinterpret_cast<const uint16_t*>(a.k) + kvh * D;
+  const uint16_t* vbase = reinterpret_cast<const uint16_t*>(a.v) + kvh * D;
+  const uint32_t loff = (uint32_t)(slot * tok + 8 * ck) * 2u;   // bytes; < 16 * tok * 2
+
+  typename W::Regs rg;
+  // Loads of page pg of the partition (pg < npages <= kMaxPages).
+  auto load_page = [&](typename W::Regs& r, int pg) {
+    pg = min(pg, kMaxPages - 1);
+    const int64_t b0 = safe_block(__builtin_amdgcn_readlane(idv, pg), a.NB) * kPage;
+    const char* kp = reinterpret_cast<const char*>(kbase + b0 * tok);
+    const char* vp = reinterpret_cast<const char*>(vbase + b0 * tok);
+#pragma unroll
+    for (int u = 0; u < kLi; ++u)
+      r.k[u] = load16_stream(kp + (int64_t)u * kTpi * tok * 2 + loff);
+#pragma unroll
+    for (int u = 0; u < kLi; ++u)
+      r.v[u] = load16_stream(vp + (int64_t)u * kTpi * tok * 2 + loff);
+  };
+  // Registers -> LDS, rows as loaded.
+  auto store_page = [&](const typename W::Regs& r) {
+#pragma unroll
+    for (int u = 0; u < kLi; ++u) {
+      *reinterpret_cast<uint4*>(&w.k[kTpi * u + slot][8 * ck]) = r.k[u];
+      *reinterpret_cast<uint4*>(&w.v[kTpi * u + slot][8 * ck]) = r.v[u];
+    }
+  };
+
+#pragma unroll
+  for (int d = 0; d < kDT; ++d)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[d][i] = 0.0f;
+  m = kNegBig;
+  l = 0.0f;
+
+  load_page(rg, 0);
+  for (int pg = 0; pg < npages; ++pg) {
+    {
+      store_page(rg);
+      // the next page's loads fly during this page's arithmetic; none past
+      // the last page
+      if (pg + 1 < npages) load_page(rg, pg + 1);   // wave-uniform
+
+      // S^T: lane l gets tokens 4g + i of this page for head j
+      float4x sa[kQS];
+#pragma unroll
+      for (int q = 0; q < kQS; ++q) sa[q] = float4x{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int st = 0; st < kKS; ++st) {
+        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(&w.k[j][32 * st + 8 * g]);
+#pragma unroll
+        for (int q = 0; q < kQS; ++q)
+          sa[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[q][st], sa[q], 0, 0, 0);
+      }
+      float s[4];
+      const int t0 = lo + pg * kPage + 4 * g;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float x = kCols ? sa[0][i] + dpp<kDppRowRor8>(sa[0][i]) : sa[0][i] + sa[kQS - 1][i];
+        s[i] = t0 + i < hi ? x : -INFINITY;
+      }
+
+      // online softmax of head j; the max is raised only when it grows by > 8
+      float mx = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+      mx = max_across_groups(mx);
+      const float m_new = mx > m + kSlack ? mx : m;
+      if (__builtin_amdgcn_ballot_w64(m_new != m) != 0) {
+        const float corr = fast_exp2(m - m_new);    // 1 for heads that keep m
+        l *= corr;
+#pragma unroll
+        for (int d = 0; d < kDT; ++d)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) o[d][i] *= corr;
+        m = m_new;
+      }
+      short4x pf[kQS];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float p = fast_exp2(s[i] - m);        // masked tokens: exp2(-inf) = 0
+        l += p;
+        uint16_t h16, l16;
+        split_bf16(p, h16, l16);
+        if constexpr (kCols) {
+          pf[0][i] = (short)(lo_col ? l16 : h16);
+        } else {
+          pf[0][i] = (short)h16;
+          pf[1][i] = (short)l16;
+        }
+      }
+
+      // O^T += V^T . P^T, dims 16 d .. 16 d + 15 per tile
+#pragma unroll
+      for (int d = 0; d < kDT; ++d) {
+        const short4x vf = read_vt(w, d, j, g);
+#pragma unroll
+        for (int q = 0; q < kQS; ++q)
+          o[d] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vf, pf[q], o[d], 0, 0, 0);
+      }
+    }
+  }
+}
+
+template <int D, bool kCols>
+__global__ __launch_bounds__(64) void bf16mm_part_kernel(RowAttnArgs a) {
+  __shared__ PageLds<D> lds;
+  const int lane = threadIdx.x & 63;
+  const int j = lane & 15;
+  const int g = lane >> 4;
+  const int G = a.H / a.Hkv;
+  const int n_hc = (G + kSlots - 1) / kSlots;          // head chunks per KV head
+  const int n_units = a.Hkv * n_hc;
+  // One wave per workgroup, numbered unit-fastest over (row, partition, unit).
+  const int64_t gw = blockIdx.x;
+  if (gw >= (int64_t)a.rows * a.P * n_units) return;
+  const int unit = (int)(gw % n_units);
+  const int kvh = unit / n_hc;
+  const int hc = unit - kvh * n_hc;
+  const int h0 = kvh * G + hc * kSlots;
+  const int gc = min(kSlots, G - hc * kSlots);          // heads of this wave
+  const int64_t rp = gw / n_units;
+  const int row = (int)(rp / a.P);
+  const int p = (int)(rp - (int64_t)row * a.P);
+  if (a.skip && a.skip[rp]) return;                     // served by the shared-page kernel
+
+  int b, end;
+  if (!row_geometry(a, row, b, end)) return;
+  int lo = 0, hi = 0, nparts = 0;
+  const bool live = partition_range(a, end, p, lo, hi, nparts);
+  const int64_t orow0 = ((int64_t)row * a.H + h0) * D;
+  if (!live) {
+    if (end <= 0 && p == 0) {   // nothing to attend to: zero rows
+      for (int d = lane; d < gc * D; d += 64) a.out[orow0 + d] = 0.0f;
+    }
+    return;
+  }
+  float4x o[D / 16];
+  float m, l;
+  page_walk<D, kCols>(a, lds, kvh, gc, a.bt + (int64_t)b * a.MB, lo, hi, orow0, o, m, l);
+  const float lsum = sum_across_groups(l);
+  if constexpr (kCols) {   // head j < 8: hi column j plus lo column j + 8
+#pragma unroll
+    for (int d = 0; d < D / 16; ++d)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[d][i] += dpp<kDppRowRor8>(o[d][i]);
+  }
+
+  // Lane (j, g) owns dims 16 d + 4 g .. + 3 of head h0 + j.  The rows go
+  // through the page buffers (free now; one wave's LDS operations complete
+  // in order), then out with D / 4 lanes per head row.
+  constexpr int kSt = D + 4;                          // floats per staged row
+  static_assert(kSlots * kSt * sizeof(float) <= sizeof(PageLds<D>), "staging fits");
+  float* st = reinterpret_cast<float*>(&lds);
+  const bool single = nparts == 1;
+  const float sc = single ? (lsum > 0.0f ? 1.0f / lsum : 0.0f) : 1.0f;
+#pragma unroll
+  for (int d = 0; d < D / 16; ++d)
+    *reinterpret_cast<float4*>(&st[j * kSt + 16 * d + 4 * g]) =
+        make_float4(o[d][0] * sc, o[d][1] * sc, o[d][2] * sc, o[d][3] * sc);
+  const int64_t pi0 = ((int64_t)row * a.H + h0) * a.P + p;   // state of head h0
+  if (!single && g == 0 && j < gc)
+    *reinterpret_cast<float2*>(a.part_ml + 2 * (pi0 + (int64_t)j * a.P)) = make_float2(m, lsum);
+  constexpr int kLr = D / 4;                          // lanes per head row
+  constexpr int kHp = 64 / kLr;                       // head rows per pass
+  const int c4 = lane % kLr;
+  for (int hb = 0; hb < gc; hb += kHp) {              // wave-uniform
+    const int hh = hb + lane / kLr;
+    if (hh < gc) {
+      const float4 x = *reinterpret_cast<const float4*>(&st[hh * kSt + 4 * c4]);
+      float* dst = single ? a.out + orow0 + (int64_t)hh * D
+                          : a.part_acc + (pi0 + (int64_t)hh * a.P) * D;
+      *reinterpret_cast<float4*>(dst + 4 * c4) = x;
+    }
+  }
+}
+
+}  // namespace
+
+bool bf16mm_applies(const RowAttnArgs& a, int kv_dtype, int D) {
+  return kv_dtype == HS_DTYPE_BF16 && a.BS == kPage && (D == 64 || D == 128) &&
+         a.H / a.Hkv >= 2 && a.mode == 1 && a.part_tokens <= kPage * kMaxPages;
+}
+
+int64_t bf16mm_grid(const RowAttnArgs& a) {
+  const int G = a.H / a.Hkv;
+  return sat_mul(a.rows, a.P, a.Hkv, ceil_div(G, kSlots));
+}
+
+void launch_bf16mm_part(const RowAttnArgs& a, int D, hipStream_t stream) {
+  const dim3 grid((unsigned)bf16mm_grid(a)), block(64);
+  const bool cols = a.H / a.Hkv <= 8;   // one head chunk of at most 8 heads
+  if (D == 64) {
+    if (cols) hipLaunchKernelGGL((bf16mm_part_kernel<64, true>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((bf16mm_part_kernel<64, false>), grid, block, 0, stream, a);
+  } else {
+    if (cols) hipLaunchKernelGGL((bf16mm_part_kernel<128, true>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((bf16mm_part_kernel<128, false>), grid, block, 0, stream, a);
+  }
+}
+
+}  // namespace hs

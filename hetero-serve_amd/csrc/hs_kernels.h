@@ -108,6 +108,12 @@ bool gqa_mfma_applies(const RowAttnArgs& a, int kv_dtype, int D);
 int64_t gqa_mfma_grid(const RowAttnArgs& a);
 void launch_gqa_mfma_part(const RowAttnArgs& a, int kv_dtype, int D, hipStream_t stream);
 
+// Grouped-query decode of bf16 caches on the matrix cores with split bf16
+// operands (hs_decode_bf16mm.hip): fp32-grade results, no conversion.
+bool bf16mm_applies(const RowAttnArgs& a, int kv_dtype, int D);
+int64_t bf16mm_grid(const RowAttnArgs& a);
+void launch_bf16mm_part(const RowAttnArgs& a, int D, hipStream_t stream);
+
 // Query heads one decode wave serves (GQA packing): 1, 2, 4 or 8.
 int row_attn_heads_per_wave(int H, int Hkv);
 

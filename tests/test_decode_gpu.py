@@ -310,6 +310,31 @@ def test_gqa_matrix_core_table_edges():
     assert _maxerr(got[[0, 1]], want[[0, 1]]) <= 2e-3
 
 
+@pytest.mark.parametrize("H,Hkv,D", [
+    (4, 2, 128),     # G = 2, MFMA columns: hi/lo pairs of 2 heads
+    (12, 4, 64),     # G = 3: odd group, columns 3..7 and 11..15 idle
+    (24, 4, 128),    # G = 6
+    (32, 4, 128),    # G = 8: all 16 columns in use
+    (24, 2, 64),     # G = 12: hi and lo as two products
+    (48, 2, 128),    # G = 24: a chunk of 16 heads and one of 8
+])
+def test_bf16_split_operand_decode(H, Hkv, D):
+    """Grouped-query decode of a bf16 cache runs on the matrix cores with q and
+    the probabilities split into hi + lo bf16 terms: fp32-grade results
+    (5e-5 here, against 2e-3 for the fp16-operand path) for every group size
+    and both column layouts, on partitions from one page to 1024 tokens."""
+    from heteroserve import _hip
+
+    lens = [1, 15, 16, 17, 100, 511, 513, 2000]
+    pool, q, bt, ctx = _random_case(lens, H, Hkv, D, 16, torch.bfloat16, seed=H + 3 * Hkv + D)
+    kp, vp = pool[0, 0], pool[0, 1]
+    scale = D ** -0.5
+    want = _oracle(q, kp, vp, bt, ctx, scale)
+    for p in (16, 128, 1024):
+        got = _hip.decode(q, kp, vp, bt, ctx, scale, 0, partition_tokens=p)
+        assert _maxerr(got, want) <= 5e-5, (H, Hkv, D, p)
+
+
 def test_errors_are_raised_with_reference_messages():
     m1, m2, _ = _mods()
     pool, q, bt, ctx = _random_case([10], 4, 4, 64, 16, torch.float16, seed=1)
