@@ -99,20 +99,37 @@ struct DecodePlan {
 // then walks a few iterations instead of a long serial chain.  Measured on C1
 // (8 sequences, 12 heads, contexts up to 512): 20.1 us per step at 512
 // tokens, 14.8 at 64, 14.3 at 32, 15.8 at 16 (the merge grows).
-static int default_partition(int B, int H, int Hkv, int BS, int MB) {
-  const int G = H / Hkv;
-  int pt = G >= 8 && (int64_t)Hkv * (((int64_t)G + 31) / 32) <= 2
-               ? kDefaultPartition
-               : std::min(kDefaultPartition, 1024 / row_attn_heads_per_wave(H, Hkv));
+static int shrink_for_small_grid(int pt, int min_pt, int64_t waves_per_part, int BS, int MB) {
   int dev = 0;
   const int cus = hipGetDevice(&dev) == hipSuccess ? device_cu_count(dev) : 0;
   if (cus <= 0) return pt;
   const int64_t max_ctx = (int64_t)MB * BS;
-  const int64_t waves_per_part = sat_mul(B, Hkv, G / row_attn_heads_per_wave(H, Hkv));
-  while (pt > kMinDefaultPartition &&
-         sat_mul(waves_per_part, ceil_div(max_ctx, pt)) < 4 * (int64_t)cus)
+  while (pt > min_pt && sat_mul(waves_per_part, ceil_div(max_ctx, pt)) < 4 * (int64_t)cus)
     pt /= 2;
   return pt;
+}
+
+static int default_partition(int B, int H, int Hkv, int BS, int MB, int kv_dtype, int D) {
+  const int G = H / Hkv;
+  if (bf16mm_serves(kv_dtype, BS, D, H, Hkv)) {
+    // split-bf16 matrix-core decode: bf16mm_waves(G) waves share a partition
+    const int kw = bf16mm_waves(G);
+    return shrink_for_small_grid(bf16mm_default_partition(G),
+                                 std::max(kMinDefaultPartition, BS * kw),
+                                 sat_mul(B, Hkv, ceil_div(G, 16), kw), BS, MB);
+  }
+  const int pt = G >= 8 && (int64_t)Hkv * (((int64_t)G + 31) / 32) <= 2
+                     ? kDefaultPartition
+                     : std::min(kDefaultPartition, 1024 / row_attn_heads_per_wave(H, Hkv));
+  return shrink_for_small_grid(pt, kMinDefaultPartition,
+                               sat_mul(B, Hkv, G / row_attn_heads_per_wave(H, Hkv)), BS, MB);
+}
+
+// The workspace queries take no kv dtype: they size for the shortest default
+// partition any dtype gets (most partitions, largest state).
+static int default_partition_any_dtype(int B, int H, int Hkv, int BS, int MB, int D) {
+  return std::min(default_partition(B, H, Hkv, BS, MB, HS_DTYPE_F16, D),
+                  default_partition(B, H, Hkv, BS, MB, HS_DTYPE_BF16, D));
 }
 
 static int plan_decode(int BS, int MB, int num_splits, int partition_tokens, int default_pt,
@@ -196,8 +213,8 @@ size_t hs_decode_workspace_bytes(int B, int H, int Hkv, int D, int BS, int MB, i
                                  int partition_tokens) {
   DecodePlan plan;
   if (B <= 0 || H <= 0 || Hkv <= 0 || H % Hkv != 0 || D <= 0 || BS <= 0 || MB <= 0) return 0;
-  if (plan_decode(BS, MB, num_splits, partition_tokens, default_partition(B, H, Hkv, BS, MB),
-                  &plan) != HS_OK)
+  if (plan_decode(BS, MB, num_splits, partition_tokens,
+                  default_partition_any_dtype(B, H, Hkv, BS, MB, D), &plan) != HS_OK)
     return 0;
   const int64_t need = decode_ws_bytes(B, H, D, plan.P);
   return need == kTooLarge ? 0 : (size_t)need;
@@ -241,8 +258,8 @@ static int decode_common(const float* q, const void* k_cache, const void* v_cach
     return fail(HS_EUNSUPPORTED, "unsupported head_dim " + std::to_string(D));
   if (B == 0) return HS_OK;
   DecodePlan plan;
-  if ((rc = plan_decode(BS, MB, num_splits, partition_tokens, default_partition(B, H, Hkv, BS, MB),
-                        &plan)) != HS_OK)
+  if ((rc = plan_decode(BS, MB, num_splits, partition_tokens,
+                        default_partition(B, H, Hkv, BS, MB, kv_dtype, D), &plan)) != HS_OK)
     return rc;
   const int64_t need_i = decode_ws_bytes(B, H, D, plan.P);
   if (need_i == kTooLarge)
@@ -372,8 +389,8 @@ size_t hs_decode_shared_workspace_bytes(int B, int H, int Hkv, int D, int BS, in
   const size_t base = hs_decode_workspace_bytes(B, H, Hkv, D, BS, MB, 0, partition_tokens);
   if (base == 0) return 0;   // one partition per row: nothing to share
   DecodePlan plan;
-  if (plan_decode(BS, MB, 0, partition_tokens, default_partition(B, H, Hkv, BS, MB), &plan) !=
-      HS_OK)
+  if (plan_decode(BS, MB, 0, partition_tokens, default_partition_any_dtype(B, H, Hkv, BS, MB, D),
+                  &plan) != HS_OK)
     return 0;
   const int pu = H / Hkv <= 32 ? share_per_unit(H, Hkv) : 1;
   const int64_t end = share_layout((int64_t)base, B, plan.P,

@@ -13,7 +13,7 @@
 // token are one column block of an MFMA, and the kernel does a few VALU
 // instructions per page instead.  Measured on MI355X, C2's batch and contexts
 // with 32 query heads (whole decode call, bf16, D = 128): 2 / 4 / 8 / 16 / 32
-// heads per KV head 226 / 130 / 83 / 55 / 57 us, against 232 / 148 us for
+// heads per KV head 217 / 124 / 78 / 51 / 50 us, against 232 / 148 us for
 // the VALU kernel and 125 / 95 / 64 us for the fp16 matrix-core kernel
 // (hs_decode_gqa.hip), which bf16 caches no longer use.
 //
@@ -134,9 +134,10 @@ struct PageWalk {
   };
 };
 
-// One wave's pass over keys [lo, hi) (lo a multiple of 16) of block-table row
-// `bt`, for query slots j < gc whose queries start at element q_off of a.q
-// (slot j at q_off + j * D).  Returns the state in o / m / l: lane l holds
+// One wave's pass over pages first, first + step, ... of keys [lo, hi) (lo a
+// multiple of 16) of block-table row `bt`, for query slots j < gc whose
+// queries start at element q_off of a.q (slot j at q_off + j * D); no pages
+// (first past the end) leaves the empty state.  Returns the state in o / m / l: lane l holds
 // column l % 16, dims 16 * dt + 4 * (l / 16) + i of o[dt][i]; m is the running
 // max (log2 units), l this lane's share of the sum (tokens 4 * (l / 16) + i
 // of every page); the caller reduces l across the four lane groups.
@@ -151,8 +152,8 @@ struct PageWalk {
 // j and every product is taken twice, against hi and against lo.
 template <int D, bool kCols>
 __device__ inline void page_walk(const RowAttnArgs& a, PageLds<D>& w, int kvh, int gc,
-                                 const int32_t* bt, int lo, int hi, int64_t q_off,
-                                 float4x (&o)[D / 16], float& m, float& l) {
+                                 const int32_t* bt, int lo, int hi, int first, int step,
+                                 int64_t q_off, float4x (&o)[D / 16], float& m, float& l) {
   using W = PageWalk<D>;
   constexpr int kDC = W::kDC, kTpi = W::kTpi, kLi = W::kLi, kKS = W::kKS, kDT = W::kDT;
   constexpr int kQS = kCols ? 1 : 2;               // products per page and operand
@@ -240,13 +241,13 @@ __device__ inline void page_walk(const RowAttnArgs& a, PageLds<D>& w, int kvh, i
   m = kNegBig;
   l = 0.0f;
 
-  load_page(rg, 0);
-  for (int pg = 0; pg < npages; ++pg) {
+  if (first < npages) load_page(rg, first);
+  for (int pg = first; pg < npages; pg += step) {
     {
       store_page(rg);
       // the next page's loads fly during this page's arithmetic; none past
       // the last page
-      if (pg + 1 < npages) load_page(rg, pg + 1);   // wave-uniform
+      if (pg + step < npages) load_page(rg, pg + step);   // wave-uniform
 
       // S^T: lane l gets tokens 4g + i of this page for head j
       float4x sa[kQS];
@@ -307,23 +308,30 @@ __device__ inline void page_walk(const RowAttnArgs& a, PageLds<D>& w, int kvh, i
   }
 }
 
-template <int D, bool kCols>
-__global__ __launch_bounds__(64) void bf16mm_part_kernel(RowAttnArgs a) {
-  __shared__ PageLds<D> lds;
+// One workgroup per (row, partition, KV head, head chunk): kW waves take the
+// partition's pages in turn (wave w: pages w, w + kW, ...), then combine
+// their states through LDS, so the partition writes one state however many
+// waves read it.  Every early return below is workgroup-uniform (it depends
+// on blockIdx only), so all waves reach the barriers.
+template <int D, bool kCols, int kW>
+__global__ __launch_bounds__(64 * kW) void bf16mm_part_kernel(RowAttnArgs a) {
+  __shared__ PageLds<D> lds[kW];
+  __shared__ float wave_m[kW][kSlots], wave_l[kW][kSlots];
   const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
   const int j = lane & 15;
   const int g = lane >> 4;
   const int G = a.H / a.Hkv;
   const int n_hc = (G + kSlots - 1) / kSlots;          // head chunks per KV head
   const int n_units = a.Hkv * n_hc;
-  // One wave per workgroup, numbered unit-fastest over (row, partition, unit).
+  // Workgroups are numbered unit-fastest over (row, partition, unit).
   const int64_t gw = blockIdx.x;
   if (gw >= (int64_t)a.rows * a.P * n_units) return;
   const int unit = (int)(gw % n_units);
   const int kvh = unit / n_hc;
   const int hc = unit - kvh * n_hc;
   const int h0 = kvh * G + hc * kSlots;
-  const int gc = min(kSlots, G - hc * kSlots);          // heads of this wave
+  const int gc = min(kSlots, G - hc * kSlots);          // heads of this unit
   const int64_t rp = gw / n_units;
   const int row = (int)(rp / a.P);
   const int p = (int)(rp - (int64_t)row * a.P);
@@ -336,43 +344,72 @@ __global__ __launch_bounds__(64) void bf16mm_part_kernel(RowAttnArgs a) {
   const int64_t orow0 = ((int64_t)row * a.H + h0) * D;
   if (!live) {
     if (end <= 0 && p == 0) {   // nothing to attend to: zero rows
-      for (int d = lane; d < gc * D; d += 64) a.out[orow0 + d] = 0.0f;
+      for (int d = threadIdx.x; d < gc * D; d += 64 * kW) a.out[orow0 + d] = 0.0f;
     }
     return;
   }
   float4x o[D / 16];
   float m, l;
-  page_walk<D, kCols>(a, lds, kvh, gc, a.bt + (int64_t)b * a.MB, lo, hi, orow0, o, m, l);
-  const float lsum = sum_across_groups(l);
+  page_walk<D, kCols>(a, lds[wv], kvh, gc, a.bt + (int64_t)b * a.MB, lo, hi, wv, kW, orow0, o,
+                      m, l);
+  float lsum = sum_across_groups(l);
   if constexpr (kCols) {   // head j < 8: hi column j plus lo column j + 8
 #pragma unroll
     for (int d = 0; d < D / 16; ++d)
 #pragma unroll
       for (int i = 0; i < 4; ++i) o[d][i] += dpp<kDppRowRor8>(o[d][i]);
   }
+  // This wave's weight in the combined state: 2^(m - M) with M the
+  // workgroup's max for the column.
+  float sc = 1.0f;
+  if constexpr (kW > 1) {
+    if (g == 0) {
+      wave_m[wv][j] = m;
+      wave_l[wv][j] = lsum;
+    }
+    __syncthreads();
+    float mm = wave_m[0][j];
+#pragma unroll
+    for (int w = 1; w < kW; ++w) mm = fmaxf(mm, wave_m[w][j]);
+    float ll = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kW; ++w) ll += wave_l[w][j] * fast_exp2(wave_m[w][j] - mm);
+    sc = fast_exp2(m - mm);
+    m = mm;
+    lsum = ll;
+  }
 
-  // Lane (j, g) owns dims 16 d + 4 g .. + 3 of head h0 + j.  The rows go
-  // through the page buffers (free now; one wave's LDS operations complete
-  // in order), then out with D / 4 lanes per head row.
+  // Lane (j, g) owns dims 16 d + 4 g .. + 3 of head h0 + j.  Each wave's
+  // rows go to its own page buffers (free now), weighted (and normalised
+  // when the partition is the whole row); then the workgroup sums the kW
+  // copies of a head row with D / 4 lanes per row and writes it out.
   constexpr int kSt = D + 4;                          // floats per staged row
   static_assert(kSlots * kSt * sizeof(float) <= sizeof(PageLds<D>), "staging fits");
-  float* st = reinterpret_cast<float*>(&lds);
   const bool single = nparts == 1;
-  const float sc = single ? (lsum > 0.0f ? 1.0f / lsum : 0.0f) : 1.0f;
+  if (single) sc *= lsum > 0.0f ? 1.0f / lsum : 0.0f;
+  float* st = reinterpret_cast<float*>(&lds[wv]);
 #pragma unroll
   for (int d = 0; d < D / 16; ++d)
     *reinterpret_cast<float4*>(&st[j * kSt + 16 * d + 4 * g]) =
         make_float4(o[d][0] * sc, o[d][1] * sc, o[d][2] * sc, o[d][3] * sc);
   const int64_t pi0 = ((int64_t)row * a.H + h0) * a.P + p;   // state of head h0
-  if (!single && g == 0 && j < gc)
+  if (!single && wv == 0 && g == 0 && j < gc)
     *reinterpret_cast<float2*>(a.part_ml + 2 * (pi0 + (int64_t)j * a.P)) = make_float2(m, lsum);
+  if constexpr (kW > 1) __syncthreads();
   constexpr int kLr = D / 4;                          // lanes per head row
-  constexpr int kHp = 64 / kLr;                       // head rows per pass
+  constexpr int kHp = 64 / kLr;                       // head rows per wave and pass
   const int c4 = lane % kLr;
-  for (int hb = 0; hb < gc; hb += kHp) {              // wave-uniform
+  for (int hb = wv * kHp; hb < gc; hb += kW * kHp) {  // wave-uniform
     const int hh = hb + lane / kLr;
     if (hh < gc) {
-      const float4 x = *reinterpret_cast<const float4*>(&st[hh * kSt + 4 * c4]);
+      float4 x = *reinterpret_cast<const float4*>(
+          &reinterpret_cast<const float*>(&lds[0])[hh * kSt + 4 * c4]);
+#pragma unroll
+      for (int w = 1; w < kW; ++w) {
+        const float4 y = *reinterpret_cast<const float4*>(
+            &reinterpret_cast<const float*>(&lds[w])[hh * kSt + 4 * c4]);
+        x = make_float4(x.x + y.x, x.y + y.y, x.z + y.z, x.w + y.w);
+      }
       float* dst = single ? a.out + orow0 + (int64_t)hh * D
                           : a.part_acc + (pi0 + (int64_t)hh * a.P) * D;
       *reinterpret_cast<float4*>(dst + 4 * c4) = x;
@@ -382,25 +419,50 @@ __global__ __launch_bounds__(64) void bf16mm_part_kernel(RowAttnArgs a) {
 
 }  // namespace
 
-bool bf16mm_applies(const RowAttnArgs& a, int kv_dtype, int D) {
-  return kv_dtype == HS_DTYPE_BF16 && a.BS == kPage && (D == 64 || D == 128) &&
-         a.H / a.Hkv >= 2 && a.mode == 1 && a.part_tokens <= kPage * kMaxPages;
+bool bf16mm_serves(int kv_dtype, int BS, int D, int H, int Hkv) {
+  return kv_dtype == HS_DTYPE_BF16 && BS == kPage && (D == 64 || D == 128) && H / Hkv >= 2;
 }
+
+bool bf16mm_applies(const RowAttnArgs& a, int kv_dtype, int D) {
+  return bf16mm_serves(kv_dtype, a.BS, D, a.H, a.Hkv) && a.mode == 1 &&
+         a.part_tokens <= kPage * kMaxPages;
+}
+
+// Waves per partition and the default partition: each wave walks about 128
+// tokens, and groups of at most 4 query heads (the least arithmetic per
+// byte) share a 512-token partition between 4 waves, so a quarter of the
+// partition states reach HBM.  Measured on C2's batch and contexts, 32 query
+// heads (step, µs, waves x partition tokens):
+//   G = 2:  226 (1 x 256)  217 (2 x 512)  213 (4 x 512)
+//   G = 4:  129 (1 x 256)  126 (2 x 512)  123 (4 x 512)
+//   G = 8:   80 (1 x 256)   77 (2 x 256)   78 (4 x 256)
+//   G = 16:  52 (1 x 128)   50 (2 x 256)   53 (4 x 256)
+//   G = 32:  51 (1 x 128)   49 (2 x 256)   53 (4 x 256)
+int bf16mm_waves(int G) { return G <= 4 ? 4 : 2; }
+int bf16mm_default_partition(int G) { return G <= 4 ? 512 : 256; }
 
 int64_t bf16mm_grid(const RowAttnArgs& a) {
   const int G = a.H / a.Hkv;
   return sat_mul(a.rows, a.P, a.Hkv, ceil_div(G, kSlots));
 }
 
+template <int D, int kW>
+static void launch_waves(const RowAttnArgs& a, hipStream_t stream) {
+  const dim3 grid((unsigned)bf16mm_grid(a)), block(64 * kW);
+  if (a.H / a.Hkv <= 8)   // one head chunk of at most 8 heads: hi/lo as columns
+    hipLaunchKernelGGL((bf16mm_part_kernel<D, true, kW>), grid, block, 0, stream, a);
+  else
+    hipLaunchKernelGGL((bf16mm_part_kernel<D, false, kW>), grid, block, 0, stream, a);
+}
+
 void launch_bf16mm_part(const RowAttnArgs& a, int D, hipStream_t stream) {
-  const dim3 grid((unsigned)bf16mm_grid(a)), block(64);
-  const bool cols = a.H / a.Hkv <= 8;   // one head chunk of at most 8 heads
+  const bool four = bf16mm_waves(a.H / a.Hkv) == 4;
   if (D == 64) {
-    if (cols) hipLaunchKernelGGL((bf16mm_part_kernel<64, true>), grid, block, 0, stream, a);
-    else hipLaunchKernelGGL((bf16mm_part_kernel<64, false>), grid, block, 0, stream, a);
+    if (four) launch_waves<64, 4>(a, stream);
+    else launch_waves<64, 2>(a, stream);
   } else {
-    if (cols) hipLaunchKernelGGL((bf16mm_part_kernel<128, true>), grid, block, 0, stream, a);
-    else hipLaunchKernelGGL((bf16mm_part_kernel<128, false>), grid, block, 0, stream, a);
+    if (four) launch_waves<128, 4>(a, stream);
+    else launch_waves<128, 2>(a, stream);
   }
 }
 

@@ -110,7 +110,10 @@ void launch_gqa_mfma_part(const RowAttnArgs& a, int kv_dtype, int D, hipStream_t
 
 // Grouped-query decode of bf16 caches on the matrix cores with split bf16
 // operands (hs_decode_bf16mm.hip): fp32-grade results, no conversion.
-bool bf16mm_applies(const RowAttnArgs& a, int kv_dtype, int D);
+bool bf16mm_serves(int kv_dtype, int BS, int D, int H, int Hkv);   // geometry and dtype
+bool bf16mm_applies(const RowAttnArgs& a, int kv_dtype, int D);     // ... and this launch
+int bf16mm_waves(int G);                                            // waves per partition
+int bf16mm_default_partition(int G);                                // tokens, before small-grid cuts
 int64_t bf16mm_grid(const RowAttnArgs& a);
 void launch_bf16mm_part(const RowAttnArgs& a, int D, hipStream_t stream);
 

@@ -85,6 +85,9 @@ int64_t hs_choose_num_splits(int64_t num_seqs, int64_t num_heads, int64_t max_co
  * Workspace bytes hs_decode needs for these sizes (0 when it needs none).
  * num_splits and partition_tokens as for hs_decode; Hkv because the default
  * partition size depends on the GQA group (version 2 of the ABI added it).
+ * The default also depends on the kv dtype, which this query does not take:
+ * it returns the size for the shortest default any dtype gets, enough for
+ * every dtype.
  * The default also shrinks (down to 32 tokens) for small grids, from B, MB
  * and the CU count of the current device: query the size with the device
  * that will run the call current.
@@ -116,7 +119,8 @@ size_t hs_decode_workspace_bytes(int B, int H, int Hkv, int D, int BS, int MB, i
  *                     plus the merge (the fast default)
  *   partition_tokens  used when num_splits == 0; 0 = library default (512
  *                tokens, fewer for GQA groups and for grids of fewer than 4
- *                waves per CU).
+ *                waves per CU; bf16 caches with 2 or more query heads per KV
+ *                head: 512 tokens up to 4 heads per KV head, 256 above).
  *                Must be a multiple of 16.
  *   workspace    device scratch of hs_decode_workspace_bytes(...) bytes
  *                (may be NULL when that is 0).

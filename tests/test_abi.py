@@ -146,7 +146,10 @@ def test_workspace_size_formula(lib):
     then rows * H * P (max, sum) pairs; P = ceil(MB * BS / partition).  The
     default partition is 512 tokens, min(512, 1024 / G) when one wave serves
     G query heads of a GQA group (G = 1, 2, 4, 8, the largest dividing H / Hkv),
-    and 512 again when H / Hkv >= 8 and Hkv * ceil(H / Hkv / 32) <= 2."""
+    and 512 again when H / Hkv >= 8 and Hkv * ceil(H / Hkv / 32) <= 2.  bf16
+    caches with 2 or more query heads per KV head (16-token pages, head_dim
+    64/128) default to 512 tokens up to 4 heads per KV head and 256 above;
+    the query takes no dtype, so it sizes for the shorter of the two."""
     B, H, D, BS, MB = 3, 5, 128, 16, 100
 
     def ws(P):
@@ -157,7 +160,7 @@ def test_workspace_size_formula(lib):
         assert lib.hs_decode_workspace_bytes(B, H, H, D, BS, MB, 0, part) == ws(P)
     assert lib.hs_decode_workspace_bytes(B, H, H, D, BS, MB, 9, 0) == ws(9)
     H = 32
-    for Hkv, part in ((32, 512), (16, 512), (8, 256), (4, 128), (1, 512), (2, 512)):
+    for Hkv, part in ((32, 512), (16, 512), (8, 256), (4, 128), (1, 256), (2, 256)):
         P = -(-(MB * BS) // part)
         acc = (B * H * P * D * 4 + 255) // 256 * 256
         assert lib.hs_decode_workspace_bytes(B, H, Hkv, D, BS, MB, 0, 0) == acc + B * H * P * 8
