@@ -60,31 +60,45 @@ def log(*a) -> None:
 
 
 # HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE, WRITE_SIZE,
-# calibrated on a 1 GiB copy) for the default workload, in a separate profiled
-# run of this script; summarised in the committed profile below, whose table
-# this reads.
-TRAFFIC_PROFILE = ROOT / "profiles" / "decode_C2_prefill_C4_pack_C5.md"
-# The headline leg's dominant kernel, as rocprofv3 names it.
-DECODE_KERNEL = "hs::row_attn_part_kernel<hs::Bf16, 128, true, 1>"
-# C2's launch of it: 64 rows x 16 partitions of 512 tokens x 16 two-head
-# workgroups.  The PMC summary lists a kernel launched with several grid sizes
-# once per size, as "<name> [<n> workgroups]".
-DECODE_WORKGROUPS = 16384
+# calibrated on a 1 GiB copy) in separate profiled runs of this script;
+# summarised in the committed profile below, whose tables this reads.
+TRAFFIC_PROFILE = ROOT / "profiles" / "bench_legs_trace_and_traffic.md"
+# Each leg's dominant kernel as rocprofv3 names it, its grid in workgroups
+# (None: the only grid that kernel ran with) and the profile's table that
+# holds it.  C2's launch (64 rows x 16 partitions of 512 tokens x 16 two-head
+# workgroups) shares its grid with C5's plain decode, so it is profiled alone.
+LEG_KERNELS = {
+    "C2": ("hs::row_attn_part_kernel<hs::Bf16, 128, true, 1>", 16384, "C2 alone"),
+    "C3": ("hs::row_attn_part_kernel<hs::Bf16, 128, true, 1>", 32640, "every leg"),
+    "C1": ("hs::row_attn_part_kernel<_Float16, 64, true, 1>", None, "every leg"),
+    "C2-gqa": ("hs::bf16mm_part_kernel<128, true, 4>", None, "every leg"),
+    "C4": ("hs::prefill_mfma_kernel<hs::Bf16, 128, 8>", 1536, "every leg"),
+    "C5_pack": ("hs::page_copy_kernel<false, true>", None, "every leg"),
+    "C5_unpack": ("hs::page_copy_kernel<true, true>", None, "every leg"),
+}
+DECODE_KERNEL, DECODE_WORKGROUPS, _ = LEG_KERNELS["C2"]
 
 
-def profiled_traffic(kernel: str, workgroups: int):
-    """HBM read + write bytes of `kernel`'s launch of `workgroups` workgroups
-    from the committed PMC summary."""
-    names = (kernel, f"{kernel} [{workgroups} workgroups]")
+def profiled_traffic(kernel: str, workgroups, table: str = "every leg"):
+    """HBM read + write bytes of one launch of `kernel` (with `workgroups`
+    workgroups, when given) from the committed PMC summary's table `table`."""
+    names = (kernel,) if workgroups is None else (kernel, f"{kernel} [{workgroups} workgroups]")
     try:
         text = TRAFFIC_PROFILE.read_text()
-        for line in text[text.index("# HBM traffic per launch"):].splitlines():
+        text = text[text.index(f"# HBM traffic per launch: {table}"):]
+        end = text.find("\n# ", 1)
+        for line in (text if end < 0 else text[:end]).splitlines():
             cells = [c.strip(" `") for c in line.split("|")]
             if len(cells) == 7 and cells[1] in names and "." in cells[4]:
                 return int(round((float(cells[4]) + float(cells[5])) * 1e9))
     except (OSError, ValueError):
         pass
     return None
+
+
+def leg_traffic(leg: str):
+    kernel, wg, table = LEG_KERNELS[leg]
+    return profiled_traffic(kernel, wg, table)
 
 
 def cpu_model() -> str:
@@ -116,7 +130,7 @@ def roofline(kind: str, kernel: str, amount: float, kernel_ms: float, traffic=No
            "algorithmic": int(amount), "kernel_us": round(kernel_ms * 1e3, 2)}
     if traffic is not None:
         out["traffic_source"] = (f"profiles/{TRAFFIC_PROFILE.name}: rocprofv3 --pmc FETCH_SIZE + "
-                                 "WRITE_SIZE of this launch in a profiled run of bench.py")
+                                 "WRITE_SIZE of this kernel's launch in profiled runs of bench.py")
     return out
 
 
@@ -261,7 +275,8 @@ def migration_legs(steps: int, warmup: int, with_cpu: bool) -> dict:
     res = {"pack": {"us_per_step": round(pk_step * 1e3, 2),
                     "gbs": round(nbytes / (pk_kernel * 1e-3) / 1e9, 1),
                     "bytes_moved": nbytes,
-                    "roofline": roofline("hbm", "page_copy_kernel", nbytes, pk_kernel)}}
+                    "roofline": roofline("hbm", "page_copy_kernel<false, true>", nbytes, pk_kernel,
+                                         leg_traffic("C5_pack"))}}
     log(f"C5 pack: {pk_kernel * 1e3:.1f} us, {res['pack']['gbs']:.0f} GB/s")
 
     # unpack into a zeroed pool at the same ids
@@ -282,7 +297,8 @@ def migration_legs(steps: int, warmup: int, with_cpu: bool) -> dict:
                      "bytes_moved": nbytes, "bit_exact": up_exact,
                      "check": "torch GPU indexing of the unpacked pool == payload; "
                               "every other block untouched",
-                     "roofline": roofline("hbm", "page_copy_kernel", nbytes, up_kernel)}
+                     "roofline": roofline("hbm", "page_copy_kernel<true, true>", nbytes, up_kernel,
+                                          leg_traffic("C5_unpack"))}
     log(f"C5 unpack: {up_kernel * 1e3:.1f} us, {res['unpack']['gbs']:.0f} GB/s, exact={up_exact}")
 
     # plain-copy ceilings of the same 1 GiB (into their own buffer: `out`
@@ -690,7 +706,8 @@ def secondary_decode(name: str, kernel: str, steps: int, warmup: int, with_cpu: 
     res = {"us_per_step": round(dec["step_ms"] * 1e3, 2), "gbs": round(dec["step_gbs"], 1),
            "hbm_frac": round(dec["step_gbs"] / HBM_PEAK_GBS, 4),
            "config": decode_config(case, 0),
-           "roofline": roofline("hbm", kernel, dec["bytes"], dec["kernel_ms"])}
+           "roofline": roofline("hbm", kernel, dec["bytes"], dec["kernel_ms"],
+                                leg_traffic(name))}
     log(f"{name} decode: step {dec['step_ms'] * 1e3:.1f} us ({dec['step_gbs']:.0f} GB/s), "
         f"kernel {dec['kernel_ms'] * 1e3:.1f} us ({dec['kernel_gbs']:.0f} GB/s)")
     if with_cpu:
@@ -768,7 +785,7 @@ def main() -> int:
     if not args.no_secondary:
         legs = [("C1", "row_attn_part_kernel<_Float16, 64, true, 1>", True, 0),
                 ("C3", "row_attn_part_kernel<Bf16, 128, true, 1>", False, 4),
-                ("C2-gqa", "row_attn_part_kernel<Bf16, 128, true, 4>", False, 16)]
+                ("C2-gqa", "bf16mm_part_kernel<128, true, 4>", False, 16)]
         for name, kernel, batched, n_seq in legs:
             if name == headline_name:
                 continue
@@ -789,7 +806,7 @@ def main() -> int:
             "mfma_frac": round(pre["kernel_tflops"] / MFMA_F16_PEAK_TFLOPS, 4),
             "useful_flops": pre["flops"],
             "roofline": roofline("mfma", "prefill_mfma_kernel<Bf16, 128, 8>", pre["flops"],
-                                 pre["kernel_ms"]),
+                                 pre["kernel_ms"], leg_traffic("C4")),
         }
         log(f"C4 prefill: {pre['step_ms'] * 1e3:.1f} us, {pre['kernel_tflops']:.1f} TFLOP/s")
         if with_cpu:
@@ -846,8 +863,9 @@ def main() -> int:
         "config": config,
         "roofline": roofline(
             "hbm", "row_attn_part_kernel", dec["bytes"], dec["kernel_ms"],
-            profiled_traffic(DECODE_KERNEL, DECODE_WORKGROUPS)
-            if args.config == "C2" and not args.partition else None),
+            leg_traffic(args.config)
+            if args.config in LEG_KERNELS and args.config != "C2-gqa" and not args.partition
+            else None),
         "cpu_baseline": cpu,
         "max_abs_err": errors.get(headline_name),
         "parity": ("pass" if ok else "fail") if (errors or exact) else "not checked (--no-cpu)",

@@ -14,9 +14,18 @@ def test_traffic_row_of_headline_kernel_is_found():
     # roofline.traffic comes from the committed rocprofv3 summary; the row
     # must exist for the kernel the headline leg runs, and the measured HBM
     # bytes must be close to the algorithmic K+V bytes of C2 (2.4617 GB)
-    traffic = bench.profiled_traffic(bench.DECODE_KERNEL, bench.DECODE_WORKGROUPS)
+    traffic = bench.profiled_traffic(bench.DECODE_KERNEL, bench.DECODE_WORKGROUPS, "C2 alone")
     assert traffic is not None
     assert abs(traffic / 2_461_696_000 - 1.0) < 0.02
+
+
+def test_every_leg_has_a_traffic_row():
+    # each leg's roofline reads its kernel's HBM bytes from the same summary;
+    # the copy legs move exactly 2 GiB (1 GiB read + 1 GiB written)
+    for leg in bench.LEG_KERNELS:
+        assert bench.leg_traffic(leg) is not None, leg
+    for leg in ("C5_pack", "C5_unpack"):
+        assert abs(bench.leg_traffic(leg) / 2 ** 31 - 1.0) < 0.01
 
 
 def test_more_than_one_gpu_is_refused():
