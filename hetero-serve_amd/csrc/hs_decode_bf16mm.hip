@@ -92,9 +92,10 @@ struct PageLds {
 template <int D>
 __device__ inline short4x read_vt(const PageLds<D>& w, int dt, int j, int g) {
   typedef __attribute__((address_space(3))) short4x lds_short4x;
-  const uint16_t* p = &w.v[4 * g + (j >> 2)][16 * dt + 4 * (j & 3)];
-  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (lds_short4x*)((__attribute__((address_space(3))) void*)(uintptr_t)p));
+  // a C-style cast keeps the LDS address arithmetic visible, so the constant
+  // part of the address goes into the instruction's offset field
+  const lds_short4x* p = (const lds_short4x*)(&w.v[4 * g + (j >> 2)][16 * dt + 4 * (j & 3)]);
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(const_cast<lds_short4x*>(p));
 }
 
 // x = hi + lo with hi, lo bf16 (RNE); returns the bf16 bit patterns.

@@ -23,9 +23,10 @@
 // registers for the whole walk).  The accumulator then has one query per
 // lane and 16 keys per lane in registers, which is exactly the layout of the
 // B operand of O^T = V^T . P^T, so the probabilities P go from the softmax to
-// the second MFMA without leaving registers; V^T (A operand) comes from a
-// transposed copy of the V tile in LDS.  O^T accumulates one query per lane,
-// so the online-softmax rescale is a per-lane scalar multiply.
+// the second MFMA without leaving registers; V^T (A operand) is read from the
+// token-major V tile in LDS with gfx950's transposing ds_read_b64_tr_b16.
+// O^T accumulates one query per lane, so the online-softmax rescale is a
+// per-lane scalar multiply.
 //
 // Key order inside a tile.  A 32x32 accumulator gives lane half h the key rows
 // 8g + 4h + m (g = 0..3, m = 0..3) in registers 4g + m.  The P.V operand
@@ -65,7 +66,7 @@ constexpr int kRowsPerWave = 32;             // one 32-row MFMA tile per wave
 constexpr int kBN = 64;                      // keys per LDS tile (four pages), a multiple of 32
 constexpr int kXcds = 8;
 constexpr int kKPad = 8;                     // halves of padding per LDS K row
-constexpr int kVPad = 8;                     // halves of padding per LDS V^T row
+constexpr int kVPad = 16;                    // halves of padding per LDS V row
 constexpr float kRescaleSlack = 8.0f;        // log2 units
 constexpr int kMaxRanked = 256;              // sequences a workgroup ranks itself
 constexpr int kMaxSplit = 4;                 // key-range parts of one query tile
@@ -108,11 +109,37 @@ struct PrefillArgs {
   float2* part_ml;       // [n_split, B, rows_cap, H]
 };
 
+// K rows are read as 16-byte fragments (row j by lane j), V rows by the
+// transposing read (four rows by each group of 16 lanes); the two paddings
+// keep each pattern free of bank conflicts.
 template <int D>
 struct PrefillTileLds {
   _Float16 k[kBN][D + kKPad];       // K tile, row r holds key swap23(r)
-  _Float16 vt[D][kBN + kVPad];      // V tile transposed
+  _Float16 v[kBN][D + kVPad];       // V tile, row r holds key r
 };
+
+// V^T fragment (A operand of the 32x32x16 product) for dims 32 d .. 32 d + 31
+// and keys k0 + 8 hh .. k0 + 8 hh + 7: lane (j, hh) gets V[k0 + 8 hh + e][32 d + j],
+// e = 0..7.  ds_read_b64_tr_b16 transposes inside each group of 16 lanes:
+// lane i supplies 8 bytes of row i / 4 of a 4 x 16 block and receives column
+// i (lane layout checked on gfx950); two reads give the eight keys.
+template <int D>
+__device__ inline half8 vt_fragment(const PrefillTileLds<D>& t, int d, int k0, int j, int hh) {
+  typedef __fp16 half4x __attribute__((__vector_size__(4 * sizeof(__fp16))));
+  typedef __attribute__((address_space(3))) half4x lds_half4x;
+  typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+  const int i = j & 15;
+  // C-style casts keep the LDS address arithmetic visible, so the constant
+  // part of the address goes into the instructions' offset field
+  const lds_half4x* lo_p =
+      (const lds_half4x*)(&t.v[k0 + 8 * hh + (i >> 2)][32 * d + (j & 16) + 4 * (i & 3)]);
+  const lds_half4x* hi_p =
+      (const lds_half4x*)(&t.v[k0 + 8 * hh + 4 + (i >> 2)][32 * d + (j & 16) + 4 * (i & 3)]);
+  const half4x lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16(const_cast<lds_half4x*>(lo_p));
+  const half4x hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16(const_cast<lds_half4x*>(hi_p));
+  return __builtin_shufflevector(__builtin_bit_cast(f16x4, lo), __builtin_bit_cast(f16x4, hi),
+                                 0, 1, 2, 3, 4, 5, 6, 7);
+}
 
 // The producer: how the first half of a workgroup's waves (256 threads at
 // head dim 128) move one K/V tile from the paged cache through registers
@@ -125,11 +152,10 @@ struct PrefillTileLds {
 //      neighbouring lanes read one 256-byte head row, and every load of a
 //      wave falls in a single page, so the page base is a scalar and each lane
 //      keeps one 32-bit offset for the whole walk.
-//   V: the thread owns kG consecutive keys kG*(tid % (64/kG)) of the 8 dims
-//      8*(tid / (64/kG)), so that its transposed LDS store for one dim is one
-//      kG*2-byte write and 64/kG neighbouring lanes fill one V^T row segment.
-//      Its kG keys lie in one page: one block id and one base per tile.
-// The block ids of a tile are fetched by one vector load, a tile ahead.
+//   V: the same chunks as K (same pages, same lane offsets), stored
+//      token-major.
+// The block ids of a tile are fetched by one vector load, a tile ahead: lane
+// L holds the id of page L * kG / 16 (kG = 64 / (keys per lane group)).
 template <int D, int W>
 struct Producer {
   static constexpr int kDC = D / 8;                         // 16-byte chunks per head row
@@ -146,17 +172,16 @@ struct Producer {
   // One tile in flight from global memory.
   struct Regs {
     uint4 k[kKChunks];
-    uint4 v[kG];
+    uint4 v[kKChunks];
   };
 
-  int vid[2];          // block id of this lane's V page for tiles of parity 0 / 1
+  int vid[2];          // page ids of the tiles of parity 0 / 1 (lane L: page vpage(L))
   float chk;           // range check of the fp16 words this thread wrote (bf16 caches)
 
   // per-thread constants
   uint32_t koff;       // byte offset of this lane's K chunk inside a page (+ head)
   int kpage0;          // page of K chunk 0 (wave-uniform)
-  int vpage;           // page of this lane's V keys
-  int64_t voff;        // element offset of this lane's V chunk inside a page (+ head)
+  int vpage;           // page whose id this lane fetches
   int64_t tok;         // elements between consecutive tokens of a page
 
   __device__ inline void init(const PrefillArgs& a, int wave, int kvh) {
@@ -166,9 +191,7 @@ struct Producer {
     const int t_k = tid / kDC;
     koff = (uint32_t)(((t_k % 16) * tok + kvh * D + (tid % kDC) * 8) * 2);
     kpage0 = wave * 64 / (16 * kDC);
-    const int key0 = kG * (tid % kGroups);
-    vpage = key0 / 16;
-    voff = (key0 % 16) * tok + kvh * D + (tid / kGroups) * 8;
+    vpage = kG * (tid % kGroups) / 16;
   }
 
   // One vector load per tile: lane L reads the id of the page its V keys are
@@ -191,9 +214,14 @@ struct Producer {
 
   template <typename T, int kSlot>
   __device__ inline void load_v(const PrefillArgs& a, Regs& r) const {
-    const T* p = reinterpret_cast<const T*>(a.v) + safe_block(vid[kSlot], a.NB) * tok * 16 + voff;
 #pragma unroll
-    for (int g = 0; g < kG; ++g) r.v[g] = load16(p + g * tok);
+    for (int u = 0; u < kKChunks; ++u) {
+      const int page = kpage0 + u * (kKeysPerU / 16);            // wave-uniform
+      const int vid_u = __builtin_amdgcn_readlane(vid[kSlot], page * 16 / kG);
+      const char* base = reinterpret_cast<const char*>(a.v) +
+                         safe_block(vid_u, a.NB) * tok * 16 * (int64_t)sizeof(T);
+      r.v[u] = load16(base + koff);
+    }
   }
 
   template <typename T, int kSlot>
@@ -203,7 +231,7 @@ struct Producer {
     load_v<T, kSlot>(a, r);
   }
 
-  // Registers -> LDS (fp16; K with the bit-2/3 row swap, V transposed).
+  // Registers -> LDS (fp16; K with the bit-2/3 row swap, V in key order).
   // Only a bf16 cache can hold values fp16 cannot; those words are checked.
   // The empty asm pins each check next to its conversion: left free, the
   // compiler sinks the checks into the next tile and keeps the converted
@@ -223,21 +251,12 @@ struct Producer {
 
   template <typename T>
   __device__ inline void store_v(PrefillTileLds<D>& s, const Regs& r) {
-    static_assert(kG == 2 || kG == 4, "V keys per thread");
-    const int key0 = kG * (threadIdx.x % kGroups);
-    const int dc = threadIdx.x / kGroups;
+    const int t_k = threadIdx.x / kDC;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      _Float16* dst = &s.vt[dc * 8 + e][key0];
-      if constexpr (kG == 4) {
-        const uint32_t w0 = pack_col<T>(r.v[0], r.v[1], e), w1 = pack_col<T>(r.v[2], r.v[3], e);
-        if constexpr (std::is_same_v<T, Bf16>) fold_check(f16_check(w0, w1, 0.0f));
-        *reinterpret_cast<uint2*>(dst) = make_uint2(w0, w1);
-      } else {
-        const uint32_t w0 = pack_col<T>(r.v[0], r.v[1], e);
-        if constexpr (std::is_same_v<T, Bf16>) fold_check(f16_check(w0, w0, 0.0f));
-        *reinterpret_cast<uint32_t*>(dst) = w0;
-      }
+    for (int u = 0; u < kKChunks; ++u) {
+      const uint4 h = to_f16x8<T>(r.v[u]);
+      if constexpr (std::is_same_v<T, Bf16>) fold_check(f16_check(h, 0.0f));
+      *reinterpret_cast<uint4*>(&s.v[t_k + u * kKeysPerU][(threadIdx.x % kDC) * 8]) = h;
     }
   }
 
@@ -580,8 +599,7 @@ void prefill_mfma_kernel(PrefillArgs a) {
         for (int kc = 0; kc < 2; ++kc)
   #pragma unroll
           for (int d = 0; d < kDB; ++d)
-            vf[kc][d] =
-                *reinterpret_cast<const half8*>(&t.vt[d * 32 + j][kb * 32 + kc * 16 + 8 * hh]);
+            vf[kc][d] = vt_fragment<D>(t, d, kb * 32 + kc * 16, j, hh);
         if (kb + 1 < kNKB) {
   #pragma unroll
           for (int c = 0; c < kDC16; ++c)
