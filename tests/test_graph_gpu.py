@@ -53,6 +53,10 @@ def test_decode_prefill_and_pack_replay_bit_exact():
     dec = build_decode("g", np.array([1, 300, 1100, 4000, 17]), 8, 8, 128, 800,
                        torch.bfloat16, DEV, seed=12)
     dec_args = (dec.q, dec.k_cache, dec.v_cache, dec.block_tables, dec.context_lens, dec.scale)
+    # grouped-query decode of a bf16 cache: the split-bf16 matrix-core kernel
+    gqa = build_decode("g", np.array([5, 700, 2500, 16]), 32, 8, 128, 300,
+                       torch.bfloat16, DEV, seed=14)
+    gqa_args = (gqa.q, gqa.k_cache, gqa.v_cache, gqa.block_tables, gqa.context_lens, gqa.scale)
     # a single chunk: a small grid, so the MFMA prefill splits the key range
     # and runs its merge kernel too
     pre = build_prefill("g", np.array([700]), np.array([300]), 8, 8, 128, 80,
@@ -65,6 +69,7 @@ def test_decode_prefill_and_pack_replay_bit_exact():
                          dtype=pool.dtype, device=DEV)
 
     want_dec = paged_attn.paged_attention(*dec_args)
+    want_gqa = paged_attn.paged_attention(*gqa_args)
     want_pre = paged_attn_wmma.paged_attention_prefill_wmma(*pre_args)
     _hip.kv_pack(pool, ids, packed)
     want_pack = packed.clone()
@@ -72,9 +77,10 @@ def test_decode_prefill_and_pack_replay_bit_exact():
 
     def step():
         d = paged_attn.paged_attention(*dec_args)
+        g = paged_attn.paged_attention(*gqa_args)
         p = paged_attn_wmma.paged_attention_prefill_wmma(*pre_args)
         _hip.kv_pack(pool, ids, packed)
-        return d, p
+        return d, g, p
 
-    graph, (d, p) = _capture(step)
-    _replays_match(graph, [d, p, packed], [want_dec, want_pre, want_pack])
+    graph, (d, g, p) = _capture(step)
+    _replays_match(graph, [d, g, p, packed], [want_dec, want_gqa, want_pre, want_pack])
