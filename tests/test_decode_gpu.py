@@ -335,6 +335,28 @@ def test_bf16_split_operand_decode(H, Hkv, D):
         assert _maxerr(got, want) <= 5e-5, (H, Hkv, D, p)
 
 
+def test_bf16_split_operand_decode_fuzz():
+    """Seeded random group sizes (2..32 query heads per KV head, odd ones
+    included), head dims, batch shapes and partition lengths for the split-bf16
+    matrix-core decode, each against the oracle at 5e-5."""
+    from heteroserve import _hip
+
+    rng = np.random.default_rng(2024)
+    groups = [(4, 2), (6, 3), (8, 2), (12, 4), (15, 3), (20, 4), (24, 3), (32, 8), (40, 5),
+              (48, 3), (64, 4), (64, 2)]
+    for case in range(16):
+        H, Hkv = groups[case % len(groups)]
+        D = int(rng.choice([64, 128]))
+        lens = [int(x) for x in rng.integers(1, 1500, size=int(rng.integers(1, 7)))]
+        pt = int(rng.choice([0, 16, 48, 256, 1024]))
+        pool, q, bt, ctx = _random_case(lens, H, Hkv, D, 16, torch.bfloat16, seed=100 + case)
+        kp, vp = pool[0, 0], pool[0, 1]
+        scale = D ** -0.5
+        got = _hip.decode(q, kp, vp, bt, ctx, scale, 0, partition_tokens=pt)
+        want = _oracle(q, kp, vp, bt, ctx, scale)
+        assert _maxerr(got, want) <= 5e-5, (case, H, Hkv, D, lens, pt)
+
+
 def test_errors_are_raised_with_reference_messages():
     m1, m2, _ = _mods()
     pool, q, bt, ctx = _random_case([10], 4, 4, 64, 16, torch.float16, seed=1)
