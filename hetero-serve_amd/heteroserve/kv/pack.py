@@ -209,21 +209,26 @@ def block_table_tensor(tables, pad_to=None, device="cuda"):
     int32 ``[len(tables), width]`` table, -1 padded, ``width = pad_to`` or the
     longest table (1 when there are no tables); longer tables are truncated.
     One host-to-device copy of all ids instead of one per sequence."""
+    import itertools
+
     import numpy as np
     import torch
 
-    tables = [list(t) for t in tables]
+    if not isinstance(tables, (list, tuple)):
+        tables = list(tables)
     width = pad_to or max((len(t) for t in tables), default=1)
     B = len(tables)
     out = torch.empty((B, width), dtype=torch.int32, device=device)
     if B == 0 or width == 0:
         return out
-    rows = [np.asarray(t[:width], dtype=np.int64) for t in tables]
-    flat = np.concatenate(rows) if rows else np.zeros(0, np.int64)
+    # one conversion of all ids (the Python-int conversion is the host cost)
+    lens = [min(len(t), width) for t in tables]
+    flat = np.array(list(itertools.chain.from_iterable(
+        t if len(t) <= width else list(t)[:width] for t in tables)), dtype=np.int64)
     if flat.size and (flat.min() < -2 ** 31 or flat.max() >= 2 ** 31):
         raise RuntimeError("value cannot be converted to type int32 without overflow")
     off = np.zeros(B + 1, dtype=np.int64)
-    np.cumsum([r.size for r in rows], out=off[1:])
+    np.cumsum(lens, out=off[1:])
     packed = torch.from_numpy(np.concatenate([off, flat]).astype(np.int32)).to(out.device)
     _hip.block_tables(packed, B, width, out)
     return out

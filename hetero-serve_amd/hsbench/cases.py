@@ -261,6 +261,16 @@ def c5_decode(device, dtype=None) -> PagedCase:
     return case
 
 
+def c5_decode_tables():
+    """C5's decode batch without its pool: (context lengths, block lists),
+    the same seeded values c5_decode builds."""
+    rng = np.random.default_rng(4)
+    ctx = rng.integers(256, 4096, size=255, endpoint=True)
+    shared = rng.choice(C5_POOL_BLOCKS, size=1024 // BLOCK_SIZE, replace=False).tolist()
+    share = np.arange(255) % 2 == 0
+    return ctx, _tables(rng, ctx, C5_POOL_BLOCKS, shared, share)
+
+
 def c5_prefill(device, dtype=None) -> PagedCase:
     torch = _torch()
     rng = np.random.default_rng(40)
