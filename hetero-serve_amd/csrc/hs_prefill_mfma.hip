@@ -66,7 +66,12 @@ constexpr int kRowsPerWave = 32;             // one 32-row MFMA tile per wave
 constexpr int kBN = 64;                      // keys per LDS tile (four pages), a multiple of 32
 constexpr int kXcds = 8;
 constexpr int kKPad = 8;                     // halves of padding per LDS K row
-constexpr int kVPad = 16;                    // halves of padding per LDS V row
+// Halves of padding per LDS V row.  A transposing read of V^T fragments has
+// each 32-lane half of the wave read 4 rows x 64 bytes (two 16-lane groups,
+// adjacent 16-dim column blocks); a row stride of 16 or 48 dwords mod 64 puts
+// those 4 rows on disjoint 16-bank ranges.
+template <int D>
+constexpr int v_pad() { return D == 32 ? 0 : 32; }
 constexpr float kRescaleSlack = 8.0f;        // log2 units
 constexpr int kMaxRanked = 256;              // sequences a workgroup ranks itself
 constexpr int kMaxSplit = 4;                 // key-range parts of one query tile
@@ -115,7 +120,7 @@ struct PrefillArgs {
 template <int D>
 struct PrefillTileLds {
   _Float16 k[kBN][D + kKPad];       // K tile, row r holds key swap23(r)
-  _Float16 v[kBN][D + kVPad];       // V tile, row r holds key r
+  _Float16 v[kBN][D + v_pad<D>()];  // V tile, row r holds key r
 };
 
 // V^T fragment (A operand of the 32x32x16 product) for dims 32 d .. 32 d + 31
