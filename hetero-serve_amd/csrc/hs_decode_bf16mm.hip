@@ -26,38 +26,42 @@
 // in the fp32 accumulators, so the result matches fp32 arithmetic to about
 // 2^-16 relative (the reference's kernels compute in fp32).
 //
-// Work decomposition.  One wave serves up to 16 query heads of one KV head
-// for one (row, partition) and walks the partition one 16-token page at a
-// time:
+// Work decomposition.  A workgroup serves up to 16 query heads of one KV head
+// for one (row, partition); its kW waves (4 for up to 4 heads per KV head, 2
+// above) take the partition's 16-token pages in turn, and each wave computes
+// per page:
 //   S^T = K . Q^T    v_mfma_f32_16x16x32_bf16, K (16 tokens x 32 dims, from
 //                    LDS) the A operand, Q^T (heads) the B operand, held in
-//                    registers as hi and lo; D / 32 k-steps, two products each
+//                    registers as hi and lo terms; D / 32 k-steps
 //   O^T += V^T . P^T v_mfma_f32_16x16x16_bf16, V^T (16 dims x 16 tokens, read
 //                    transposed from the token-major LDS copy by
 //                    ds_read_b64_tr_b16) the A operand, P^T the B operand.  The S^T
-//                    accumulator gives lane l the tokens 4(l/16) + i of head
+//                    accumulator gives lane l the tokens 4(l/16) + i of column
 //                    l % 16, which is exactly the B-operand layout of the
 //                    second product, so probabilities never leave registers;
-//                    and O^T has head l % 16 in lane l too, so the online
+//                    and O^T has column l % 16 in lane l too, so the online
 //                    rescale and the final normalisation are per-lane scalars.
 // Pages are loaded coalesced (D / 8 lanes per head row of one token, 16 bytes
 // each) into registers one page ahead of the one being computed, then
 // written to the wave's own LDS token-major as they came (bf16 needs no
-// conversion).  No barriers: each wave owns its LDS and its LDS operations
-// complete in order.
+// conversion); a wave's LDS operations complete in order, so the walk needs
+// no barriers.  At the end the waves combine their (m, l, O) through LDS
+// (two barriers) and the workgroup writes one partition state: a quarter
+// (or half) of the states that one-wave partitions of the same length would
+// write, which is most of what separated this kernel from its own loads
+// (measured on MI355X, 8 KV heads: 16 of 122 us went to the states).
 //
-// Workgroups are single waves.  The hardware deals workgroups to the eight
-// XCDs round-robin by workgroup id, and the waves are numbered unit-fastest,
-// so the KV heads of one (row, partition) land on different XCDs and every
-// XCD gets an equal share of each row.  With four-wave workgroups on
-// neighbouring KV heads, the XCD a unit ran on depended on the partition
-// index, and the early partitions (live in every row) piled up on a few XCDs
-// (measured on MI355X: 160 -> 138 us on C2's geometry with 8 KV heads).
+// Grid order.  The hardware deals workgroups to the eight XCDs round-robin by
+// workgroup id, and workgroups are numbered unit-fastest (unit = KV head and
+// head chunk), so the units of one (row, partition) land on different XCDs
+// and every XCD gets an equal share of each row.  Four one-KV-head waves per
+// workgroup instead made the XCD depend on the partition index, and the
+// early partitions (live in every row) piled up on a few XCDs (160 against
+// 138 us).
 //
 // The partition states (m, l, un-normalised acc) have the VALU kernel's
 // layout and meaning, and the same merge kernel combines them; they are
-// written through the wave's LDS so each head's D floats go out as whole
-// 128-byte lines.
+// written through LDS so each head's D floats go out as whole 128-byte lines.
 #include "hs_kernels.h"
 
 namespace hs {
@@ -138,10 +142,11 @@ struct PageWalk {
 // One wave's pass over pages first, first + step, ... of keys [lo, hi) (lo a
 // multiple of 16) of block-table row `bt`, for query slots j < gc whose
 // queries start at element q_off of a.q (slot j at q_off + j * D); no pages
-// (first past the end) leaves the empty state.  Returns the state in o / m / l: lane l holds
-// column l % 16, dims 16 * dt + 4 * (l / 16) + i of o[dt][i]; m is the running
-// max (log2 units), l this lane's share of the sum (tokens 4 * (l / 16) + i
-// of every page); the caller reduces l across the four lane groups.
+// (first past the end) leaves the empty state.  Returns the state in o / m /
+// l: lane l holds column l % 16, dims 16 * dt + 4 * (l / 16) + i of o[dt][i];
+// m is the running max (log2 units), l this lane's share of the sum (tokens
+// 4 * (l / 16) + i of every page); the caller reduces l across the four lane
+// groups.
 //
 // kCols (gc <= 8): the hi and lo terms are separate MFMA columns instead of
 // separate products: column c < 8 carries the hi term of head c, column
@@ -244,67 +249,65 @@ __device__ inline void page_walk(const RowAttnArgs& a, PageLds<D>& w, int kvh, i
 
   if (first < npages) load_page(rg, first);
   for (int pg = first; pg < npages; pg += step) {
-    {
-      store_page(rg);
-      // the next page's loads fly during this page's arithmetic; none past
-      // the last page
-      if (pg + step < npages) load_page(rg, pg + step);   // wave-uniform
+    store_page(rg);
+    // the next page's loads fly during this page's arithmetic; none past
+    // the last page
+    if (pg + step < npages) load_page(rg, pg + step);   // wave-uniform
 
-      // S^T: lane l gets tokens 4g + i of this page for head j
-      float4x sa[kQS];
+    // S^T: lane l gets tokens 4g + i of this page for column j
+    float4x sa[kQS];
 #pragma unroll
-      for (int q = 0; q < kQS; ++q) sa[q] = float4x{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int q = 0; q < kQS; ++q) sa[q] = float4x{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int st = 0; st < kKS; ++st) {
-        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(&w.k[j][32 * st + 8 * g]);
+    for (int st = 0; st < kKS; ++st) {
+      const bf16x8 kf = *reinterpret_cast<const bf16x8*>(&w.k[j][32 * st + 8 * g]);
 #pragma unroll
-        for (int q = 0; q < kQS; ++q)
-          sa[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[q][st], sa[q], 0, 0, 0);
-      }
-      float s[4];
-      const int t0 = lo + pg * kPage + 4 * g;
+      for (int q = 0; q < kQS; ++q)
+        sa[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[q][st], sa[q], 0, 0, 0);
+    }
+    float s[4];
+    const int t0 = lo + pg * kPage + 4 * g;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float x = kCols ? sa[0][i] + dpp<kDppRowRor8>(sa[0][i]) : sa[0][i] + sa[kQS - 1][i];
-        s[i] = t0 + i < hi ? x : -INFINITY;
-      }
+    for (int i = 0; i < 4; ++i) {
+      const float x = kCols ? sa[0][i] + dpp<kDppRowRor8>(sa[0][i]) : sa[0][i] + sa[kQS - 1][i];
+      s[i] = t0 + i < hi ? x : -INFINITY;
+    }
 
-      // online softmax of head j; the max is raised only when it grows by > 8
-      float mx = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-      mx = max_across_groups(mx);
-      const float m_new = mx > m + kSlack ? mx : m;
-      if (__builtin_amdgcn_ballot_w64(m_new != m) != 0) {
-        const float corr = fast_exp2(m - m_new);    // 1 for heads that keep m
-        l *= corr;
+    // online softmax of column j; the max is raised only when it grows by > 8
+    float mx = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+    mx = max_across_groups(mx);
+    const float m_new = mx > m + kSlack ? mx : m;
+    if (__builtin_amdgcn_ballot_w64(m_new != m) != 0) {
+      const float corr = fast_exp2(m - m_new);    // 1 for heads that keep m
+      l *= corr;
 #pragma unroll
-        for (int d = 0; d < kDT; ++d)
+      for (int d = 0; d < kDT; ++d)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) o[d][i] *= corr;
-        m = m_new;
+        for (int i = 0; i < 4; ++i) o[d][i] *= corr;
+      m = m_new;
+    }
+    short4x pf[kQS];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float p = fast_exp2(s[i] - m);        // masked tokens: exp2(-inf) = 0
+      l += p;
+      uint16_t h16, l16;
+      split_bf16(p, h16, l16);
+      if constexpr (kCols) {
+        pf[0][i] = (short)(lo_col ? l16 : h16);
+      } else {
+        pf[0][i] = (short)h16;
+        pf[1][i] = (short)l16;
       }
-      short4x pf[kQS];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float p = fast_exp2(s[i] - m);        // masked tokens: exp2(-inf) = 0
-        l += p;
-        uint16_t h16, l16;
-        split_bf16(p, h16, l16);
-        if constexpr (kCols) {
-          pf[0][i] = (short)(lo_col ? l16 : h16);
-        } else {
-          pf[0][i] = (short)h16;
-          pf[1][i] = (short)l16;
-        }
-      }
+    }
 
-      // O^T += V^T . P^T, dims 16 d .. 16 d + 15 per tile
+    // O^T += V^T . P^T, dims 16 d .. 16 d + 15 per tile
 #pragma unroll
-      for (int d = 0; d < kDT; ++d) {
-        const short4x vf = read_vt(w, d, j, g);
+    for (int d = 0; d < kDT; ++d) {
+      const short4x vf = read_vt(w, d, j, g);
 #pragma unroll
-        for (int q = 0; q < kQS; ++q)
-          o[d] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vf, pf[q], o[d], 0, 0, 0);
-      }
+      for (int q = 0; q < kQS; ++q)
+        o[d] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vf, pf[q], o[d], 0, 0, 0);
     }
   }
 }
