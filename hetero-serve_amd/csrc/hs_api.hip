@@ -94,11 +94,17 @@ struct DecodePlan {
 // short partitions cost more than the waves it adds (MQA with 32 heads on
 // C2's geometry: 65 us at 512 tokens, 90 us at 128).
 //
-// Small grids: the partition is halved (down to 32 tokens) while the launch,
-// estimated from the table's width, has fewer than 4 waves per CU.  Each wave
-// then walks a few iterations instead of a long serial chain.  Measured on C1
-// (8 sequences, 12 heads, contexts up to 512): 20.1 us per step at 512
-// tokens, 14.8 at 64, 14.3 at 32, 15.8 at 16 (the merge grows).
+// bf16 caches with 2 or more query heads per KV head run the split-bf16
+// matrix-core decode, whose workgroups of bf16mm_waves(G) waves share a
+// partition: its own default (bf16mm_default_partition, 512 or 256 tokens)
+// applies there.
+//
+// Small grids: the partition is halved (down to 32 tokens, or one page per
+// wave) while the launch, estimated from the table's width, has fewer than 4
+// waves per CU.  Each wave then walks a few iterations instead of a long
+// serial chain.  Measured on C1 (8 sequences, 12 heads, contexts up to 512):
+// 20.1 us per step at 512 tokens, 14.8 at 64, 14.3 at 32, 15.8 at 16 (the
+// merge grows).
 static int shrink_for_small_grid(int pt, int min_pt, int64_t waves_per_part, int BS, int MB) {
   int dev = 0;
   const int cus = hipGetDevice(&dev) == hipSuccess ? device_cu_count(dev) : 0;
