@@ -66,7 +66,7 @@ COMPILE_FLAGS = [
 PER_FILE_FLAGS = {
     "hs_prefill_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=true"],
     "hs_decode_gqa.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=true"],
-    "hs_decode_bf16mm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=true"],
+    "hs_decode_splitmm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=true"],
 }
 
 

@@ -4,6 +4,7 @@
 // has one, sizes grids and workspaces, and hands off to the kernel launchers.
 // It keeps no mutable state besides a per-device cache of CU counts and the
 // thread-local error message.
+#include <algorithm>
 #include <mutex>
 #include <string>
 #include <unordered_map>
@@ -94,10 +95,10 @@ struct DecodePlan {
 // short partitions cost more than the waves it adds (MQA with 32 heads on
 // C2's geometry: 65 us at 512 tokens, 90 us at 128).
 //
-// bf16 caches with 2 or more query heads per KV head run the split-bf16
-// matrix-core decode, whose workgroups of bf16mm_waves(G) waves share a
-// partition: its own default (bf16mm_default_partition, 512 or 256 tokens)
-// applies there.
+// bf16 and fp16 caches with 2 or more query heads per KV head run the
+// split-operand matrix-core decode, whose workgroups of splitmm_waves(G)
+// waves share a partition: its own default (splitmm_default_partition, 512 or
+// 256 tokens) applies there.
 //
 // Small grids: the partition is halved (down to 32 tokens, or one page per
 // wave) while the launch, estimated from the table's width, has fewer than 4
@@ -117,10 +118,10 @@ static int shrink_for_small_grid(int pt, int min_pt, int64_t waves_per_part, int
 
 static int default_partition(int B, int H, int Hkv, int BS, int MB, int kv_dtype, int D) {
   const int G = H / Hkv;
-  if (bf16mm_serves(kv_dtype, BS, D, H, Hkv)) {
-    // split-bf16 matrix-core decode: bf16mm_waves(G) waves share a partition
-    const int kw = bf16mm_waves(G);
-    return shrink_for_small_grid(bf16mm_default_partition(G),
+  if (splitmm_serves(kv_dtype, BS, D, H, Hkv)) {
+    // split-operand matrix-core decode: splitmm_waves(G) waves share a partition
+    const int kw = splitmm_waves(G);
+    return shrink_for_small_grid(splitmm_default_partition(G),
                                  std::max(kMinDefaultPartition, BS * kw),
                                  sat_mul(B, Hkv, ceil_div(G, 16), kw), BS, MB);
   }
@@ -134,8 +135,9 @@ static int default_partition(int B, int H, int Hkv, int BS, int MB, int kv_dtype
 // The workspace queries take no kv dtype: they size for the shortest default
 // partition any dtype gets (most partitions, largest state).
 static int default_partition_any_dtype(int B, int H, int Hkv, int BS, int MB, int D) {
-  return std::min(default_partition(B, H, Hkv, BS, MB, HS_DTYPE_F16, D),
-                  default_partition(B, H, Hkv, BS, MB, HS_DTYPE_BF16, D));
+  return std::min({default_partition(B, H, Hkv, BS, MB, HS_DTYPE_F32, D),
+                   default_partition(B, H, Hkv, BS, MB, HS_DTYPE_F16, D),
+                   default_partition(B, H, Hkv, BS, MB, HS_DTYPE_BF16, D)});
 }
 
 static int plan_decode(int BS, int MB, int num_splits, int partition_tokens, int default_pt,

@@ -206,19 +206,21 @@ static int launch_dim(const RowAttnArgs& a, int D, hipStream_t stream) {
 }
 
 // Launch the partition kernel (+ merge when P > 1).  Arguments are validated
-// by the caller.  Grouped-query calls that the matrix-core kernel serves go
-// there (hs_decode_gqa.hip); the rest run the VALU kernel above.  With
+// by the caller.  Grouped-query calls on 16-bit caches go to the matrix
+// cores: the split-operand kernel (hs_decode_splitmm.hip) where it serves,
+// else the fp16-operand kernel (hs_decode_gqa.hip, head_dim 32); the rest run
+// the VALU kernel above.  With
 // `shared`: the plan kernel, then the shared-page kernel, then the partition
 // kernel (which skips the grouped partitions), then the merge.  The shared
 // kernel runs first, alone: beside the partition kernel its large workgroups
 // waited for whole CUs to drain and finished last.
 int launch_row_attn(const RowAttnArgs& a, int kv_dtype, int D, hipStream_t stream,
                     const SharePlanArgs* shared) {
-  const bool bf16mm = bf16mm_applies(a, kv_dtype, D);
-  const bool mfma = !bf16mm && gqa_mfma_applies(a, kv_dtype, D);
+  const bool splitmm = splitmm_applies(a, kv_dtype, D);
+  const bool mfma = !splitmm && gqa_mfma_applies(a, kv_dtype, D);
   int64_t gx;
-  if (bf16mm) {
-    gx = bf16mm_grid(a);
+  if (splitmm) {
+    gx = splitmm_grid(a);
   } else if (mfma) {
     gx = gqa_mfma_grid(a);
   } else {
@@ -237,9 +239,9 @@ int launch_row_attn(const RowAttnArgs& a, int kv_dtype, int D, hipStream_t strea
   }
 
   int rc = HS_OK;
-  if (bf16mm) {
+  if (splitmm) {
     profile_begin(stream);
-    launch_bf16mm_part(a, D, stream);
+    launch_splitmm_part(a, kv_dtype, D, stream);
     profile_end(stream);
   } else if (mfma) {
     profile_begin(stream);

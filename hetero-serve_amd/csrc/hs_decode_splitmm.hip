@@ -1,9 +1,10 @@
-// Grouped-query decode for bf16 caches on gfx950 matrix cores, at fp32 accuracy.
+// Grouped-query decode for bf16 and fp16 caches on gfx950 matrix cores, at
+// fp32 accuracy.
 //
 // Reference: paged_attn_v2.py:75-157 (one query row per head, KV head
 // h / (H / Hkv), online softmax) and paged_attn_v3.py:75-208 (partitions
 // merged by log-sum-exp).  Same function as the VALU decode kernel
-// (hs_decode.hip); this one serves bf16 caches when two or more query heads
+// (hs_decode.hip); this one serves 16-bit caches when two or more query heads
 // share a KV head.
 //
 // Why matrix cores here.  With G query heads per KV head, the VALU kernel's
@@ -14,27 +15,32 @@
 // instructions per page instead.  Measured on MI355X, C2's batch and contexts
 // with 32 query heads (whole decode call, bf16, D = 128): 2 / 4 / 8 / 16 / 32
 // heads per KV head 217 / 124 / 78 / 51 / 50 us, against 232 / 148 us for
-// the VALU kernel and 125 / 95 / 64 us for the fp16 matrix-core kernel
-// (hs_decode_gqa.hip), which bf16 caches no longer use.
+// the VALU kernel and 125 / 95 / 64 us for the fp16-operand matrix-core
+// kernel (hs_decode_gqa.hip), which now serves only head_dim 32.
 //
-// Numerics.  The cache is bf16, so K and V go to the MFMAs as they are stored
-// (no conversion, no range limit).  The query and the probabilities are fp32;
-// each is split into two bf16 terms, x = hi + lo with hi = bf16(x) and
-// lo = bf16(x - hi), and every product is taken against both terms (as two
-// MFMA columns for up to 8 heads per KV head, as two products above that).
-// hi + lo carries 16 significant bits, the products of bf16 values are exact
-// in the fp32 accumulators, so the result matches fp32 arithmetic to about
-// 2^-16 relative (the reference's kernels compute in fp32).
+// Numerics.  K and V go to the MFMAs as they are stored (no conversion).  The
+// query and the probabilities are fp32; each is split into two terms of the
+// cache's type, x = hi + lo with hi = T(x) and lo = T(x - hi), and every
+// product is taken against both terms (as two MFMA columns for up to 8 heads
+// per KV head, as two products above that).  Products of 16-bit values are
+// exact in the fp32 accumulators, so the result matches fp32 arithmetic to
+// about 2^-16 relative for bf16 (hi + lo carries 16 significant bits) and
+// better for fp16 (22 bits).  fp16 has a narrow exponent range, so for fp16
+// caches each head's scaled query is first multiplied by a power of two that
+// puts its largest element in [2^14, 2^15) (the scores are multiplied back,
+// exactly, after the product), and the probabilities are taken 2^7 times
+// larger (at most 2^15 under the lazy rescale below): neither term then
+// overflows, and the lo terms stay clear of fp16's subnormals.
 //
 // Work decomposition.  A workgroup serves up to 16 query heads of one KV head
 // for one (row, partition); its kW waves (4 for up to 4 heads per KV head, 2
 // above) take the partition's 16-token pages in turn, and each wave computes
 // per page:
-//   S^T = K . Q^T    v_mfma_f32_16x16x32_bf16, K (16 tokens x 32 dims, from
-//                    LDS) the A operand, Q^T (heads) the B operand, held in
-//                    registers as hi and lo terms; D / 32 k-steps
-//   O^T += V^T . P^T v_mfma_f32_16x16x16_bf16, V^T (16 dims x 16 tokens, read
-//                    transposed from the token-major LDS copy by
+//   S^T = K . Q^T    v_mfma_f32_16x16x32_{bf16,f16}, K (16 tokens x 32 dims,
+//                    from LDS) the A operand, Q^T (heads) the B operand, held
+//                    in registers as hi and lo terms; D / 32 k-steps
+//   O^T += V^T . P^T v_mfma_f32_16x16x16_{bf16,f16}, V^T (16 dims x 16 tokens,
+//                    read transposed from the token-major LDS copy by
 //                    ds_read_b64_tr_b16) the A operand, P^T the B operand.  The S^T
 //                    accumulator gives lane l the tokens 4(l/16) + i of column
 //                    l % 16, which is exactly the B-operand layout of the
@@ -43,13 +49,13 @@
 //                    rescale and the final normalisation are per-lane scalars.
 // Pages are loaded coalesced (D / 8 lanes per head row of one token, 16 bytes
 // each) into registers one page ahead of the one being computed, then
-// written to the wave's own LDS token-major as they came (bf16 needs no
-// conversion); a wave's LDS operations complete in order, so the walk needs
-// no barriers.  At the end the waves combine their (m, l, O) through LDS
-// (two barriers) and the workgroup writes one partition state: a quarter
-// (or half) of the states that one-wave partitions of the same length would
-// write, which is most of what separated this kernel from its own loads
-// (measured on MI355X, 8 KV heads: 16 of 122 us went to the states).
+// written to the wave's own LDS token-major as they came (no conversion); a
+// wave's LDS operations complete in order, so the walk needs no barriers.  At
+// the end the waves combine their (m, l, O) through LDS (two barriers) and
+// the workgroup writes one partition state: a quarter (or half) of the
+// states that one-wave partitions of the same length would write, which is
+// most of what separated this kernel from its own loads (measured on MI355X,
+// 8 KV heads: 16 of 122 us went to the states).
 //
 // Grid order.  The hardware deals workgroups to the eight XCDs round-robin by
 // workgroup id, and workgroups are numbered unit-fastest (unit = KV head and
@@ -69,6 +75,8 @@ namespace hs {
 namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef short short4x __attribute__((ext_vector_type(4)));
 typedef float float4x __attribute__((ext_vector_type(4)));
 
@@ -102,11 +110,43 @@ __device__ inline short4x read_vt(const PageLds<D>& w, int dt, int j, int g) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16(const_cast<lds_short4x*>(p));
 }
 
-// x = hi + lo with hi, lo bf16 (RNE); returns the bf16 bit patterns.
-__device__ inline void split_bf16(float x, uint16_t& hi, uint16_t& lo) {
-  const __bf16 h = (__bf16)x;
+// The cache's element type and its two products.  kPBias: the probabilities
+// go to the P.V product as 2^kPBias p (fp16: p <= 2^8 under the lazy rescale,
+// so 2^15 at most); kScaleQ: each head's query is brought to [2^14, 2^15)
+// by a power of two before it is split.
+struct Bf16Ops {
+  typedef __bf16 E;
+  typedef bf16x8 E8;
+  static constexpr float kPBias = 0.0f;
+  static constexpr bool kScaleQ = false;
+  __device__ static float4x qk(E8 k, E8 q, float4x c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(k, q, c, 0, 0, 0);
+  }
+  __device__ static float4x pv(short4x v, short4x p, float4x c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(v, p, c, 0, 0, 0);
+  }
+};
+
+struct F16Ops {
+  typedef _Float16 E;
+  typedef half8 E8;
+  static constexpr float kPBias = 7.0f;
+  static constexpr bool kScaleQ = true;
+  __device__ static float4x qk(E8 k, E8 q, float4x c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(k, q, c, 0, 0, 0);
+  }
+  __device__ static float4x pv(short4x v, short4x p, float4x c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(half4, v),
+                                                 __builtin_bit_cast(half4, p), c, 0, 0, 0);
+  }
+};
+
+// x = hi + lo with hi, lo of type E (RNE); returns their bit patterns.
+template <typename E>
+__device__ inline void split16(float x, uint16_t& hi, uint16_t& lo) {
+  const E h = (E)x;
   hi = __builtin_bit_cast(uint16_t, h);
-  lo = __builtin_bit_cast(uint16_t, (__bf16)(x - (float)h));
+  lo = __builtin_bit_cast(uint16_t, (E)(x - (float)h));
 }
 
 // Both values of x across lanes l and l ^ 16, and across l and l ^ 32.
@@ -156,11 +196,16 @@ struct PageWalk {
 // probability and lane j + 8 the lo term, and o of head c is the sum of
 // columns c and c + 8 (added by the caller).  Without kCols, column j is head
 // j and every product is taken twice, against hi and against lo.
-template <int D, bool kCols>
+//
+// The state is in the ordinary units (m minus kPBias: o and l carry the
+// 2^kPBias factor of the probabilities).
+template <typename Ops, int D, bool kCols>
 __device__ inline void page_walk(const RowAttnArgs& a, PageLds<D>& w, int kvh, int gc,
                                  const int32_t* bt, int lo, int hi, int first, int step,
                                  int64_t q_off, float4x (&o)[D / 16], float& m, float& l) {
   using W = PageWalk<D>;
+  using E = typename Ops::E;
+  using E8 = typename Ops::E8;
   constexpr int kDC = W::kDC, kTpi = W::kTpi, kLi = W::kLi, kKS = W::kKS, kDT = W::kDT;
   constexpr int kQS = kCols ? 1 : 2;               // products per page and operand
   const int lane = threadIdx.x & 63;
@@ -177,10 +222,15 @@ __device__ inline void page_walk(const RowAttnArgs& a, PageLds<D>& w, int kvh, i
   const int idv = bt[min(page0 + lane, a.MB - 1)];
 
   // Q^T fragments, split: lane l holds column j's dims 32 st + 8 g .. + 7.
-  bf16x8 qf[kQS][kKS];
+  // qexp: the power of two the query was multiplied by (kScaleQ), taken back
+  // out of every score.
+  E8 qf[kQS][kKS];
+  int qexp = 0;
   {
     const float sc = hj < gc ? a.qscale : 0.0f;
     const float* qp = a.q + q_off + (int64_t)min(hj, gc - 1) * D + 8 * g;
+    float xq[kKS][8];
+    float amax = 0.0f;
 #pragma unroll
     for (int st = 0; st < kKS; ++st) {
       const float4 x0 = *reinterpret_cast<const float4*>(qp + 32 * st);
@@ -188,9 +238,24 @@ __device__ inline void page_walk(const RowAttnArgs& a, PageLds<D>& w, int kvh, i
       const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float x = xs[e] * sc;
-        const __bf16 h = (__bf16)x;
-        const __bf16 r = (__bf16)(x - (float)h);
+        xq[st][e] = xs[e] * sc;
+        amax = fmaxf(amax, fabsf(xq[st][e]));
+      }
+    }
+    if constexpr (Ops::kScaleQ) {
+      // the head's largest |element| (its D dims are spread over the four
+      // lane groups of column j); 2^qexp * amax lands in [2^14, 2^15), and
+      // a zero or non-finite head keeps qexp = 0
+      amax = max_across_groups(amax);
+      if (amax > 0.0f && __builtin_isfinite(amax)) qexp = 15 - __builtin_amdgcn_frexp_expf(amax);
+    }
+#pragma unroll
+    for (int st = 0; st < kKS; ++st) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float x = Ops::kScaleQ ? ldexpf(xq[st][e], qexp) : xq[st][e];
+        const E h = (E)x;
+        const E r = (E)(x - (float)h);
         if constexpr (kCols) {
           qf[0][st][e] = lo_col ? r : h;
         } else {
@@ -260,16 +325,16 @@ __device__ inline void page_walk(const RowAttnArgs& a, PageLds<D>& w, int kvh, i
     for (int q = 0; q < kQS; ++q) sa[q] = float4x{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int st = 0; st < kKS; ++st) {
-      const bf16x8 kf = *reinterpret_cast<const bf16x8*>(&w.k[j][32 * st + 8 * g]);
+      const E8 kf = *reinterpret_cast<const E8*>(&w.k[j][32 * st + 8 * g]);
 #pragma unroll
-      for (int q = 0; q < kQS; ++q)
-        sa[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[q][st], sa[q], 0, 0, 0);
+      for (int q = 0; q < kQS; ++q) sa[q] = Ops::qk(kf, qf[q][st], sa[q]);
     }
     float s[4];
     const int t0 = lo + pg * kPage + 4 * g;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float x = kCols ? sa[0][i] + dpp<kDppRowRor8>(sa[0][i]) : sa[0][i] + sa[kQS - 1][i];
+      float x = kCols ? sa[0][i] + dpp<kDppRowRor8>(sa[0][i]) : sa[0][i] + sa[kQS - 1][i];
+      if constexpr (Ops::kScaleQ) x = ldexpf(x, -qexp);
       s[i] = t0 + i < hi ? x : -INFINITY;
     }
 
@@ -287,12 +352,13 @@ __device__ inline void page_walk(const RowAttnArgs& a, PageLds<D>& w, int kvh, i
       m = m_new;
     }
     short4x pf[kQS];
+    const float mb = m - Ops::kPBias;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float p = fast_exp2(s[i] - m);        // masked tokens: exp2(-inf) = 0
+      const float p = fast_exp2(s[i] - mb);       // masked tokens: exp2(-inf) = 0
       l += p;
       uint16_t h16, l16;
-      split_bf16(p, h16, l16);
+      split16<E>(p, h16, l16);
       if constexpr (kCols) {
         pf[0][i] = (short)(lo_col ? l16 : h16);
       } else {
@@ -306,10 +372,10 @@ __device__ inline void page_walk(const RowAttnArgs& a, PageLds<D>& w, int kvh, i
     for (int d = 0; d < kDT; ++d) {
       const short4x vf = read_vt(w, d, j, g);
 #pragma unroll
-      for (int q = 0; q < kQS; ++q)
-        o[d] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vf, pf[q], o[d], 0, 0, 0);
+      for (int q = 0; q < kQS; ++q) o[d] = Ops::pv(vf, pf[q], o[d]);
     }
   }
+  m -= Ops::kPBias;
 }
 
 // One workgroup per (row, partition, KV head, head chunk): kW waves take the
@@ -317,8 +383,8 @@ __device__ inline void page_walk(const RowAttnArgs& a, PageLds<D>& w, int kvh, i
 // their states through LDS, so the partition writes one state however many
 // waves read it.  Every early return below is workgroup-uniform (it depends
 // on blockIdx only), so all waves reach the barriers.
-template <int D, bool kCols, int kW>
-__global__ __launch_bounds__(64 * kW) void bf16mm_part_kernel(RowAttnArgs a) {
+template <typename Ops, int D, bool kCols, int kW>
+__global__ __launch_bounds__(64 * kW) void splitmm_part_kernel(RowAttnArgs a) {
   __shared__ PageLds<D> lds[kW];
   __shared__ float wave_m[kW][kSlots], wave_l[kW][kSlots];
   const int lane = threadIdx.x & 63;
@@ -354,8 +420,8 @@ __global__ __launch_bounds__(64 * kW) void bf16mm_part_kernel(RowAttnArgs a) {
   }
   float4x o[D / 16];
   float m, l;
-  page_walk<D, kCols>(a, lds[wv], kvh, gc, a.bt + (int64_t)b * a.MB, lo, hi, wv, kW, orow0, o,
-                      m, l);
+  page_walk<Ops, D, kCols>(a, lds[wv], kvh, gc, a.bt + (int64_t)b * a.MB, lo, hi, wv, kW, orow0,
+                           o, m, l);
   float lsum = sum_across_groups(l);
   if constexpr (kCols) {   // head j < 8: hi column j plus lo column j + 8
 #pragma unroll
@@ -423,12 +489,13 @@ __global__ __launch_bounds__(64 * kW) void bf16mm_part_kernel(RowAttnArgs a) {
 
 }  // namespace
 
-bool bf16mm_serves(int kv_dtype, int BS, int D, int H, int Hkv) {
-  return kv_dtype == HS_DTYPE_BF16 && BS == kPage && (D == 64 || D == 128) && H / Hkv >= 2;
+bool splitmm_serves(int kv_dtype, int BS, int D, int H, int Hkv) {
+  return (kv_dtype == HS_DTYPE_BF16 || kv_dtype == HS_DTYPE_F16) && BS == kPage &&
+         (D == 64 || D == 128) && H / Hkv >= 2;
 }
 
-bool bf16mm_applies(const RowAttnArgs& a, int kv_dtype, int D) {
-  return bf16mm_serves(kv_dtype, a.BS, D, a.H, a.Hkv) && a.mode == 1 &&
+bool splitmm_applies(const RowAttnArgs& a, int kv_dtype, int D) {
+  return splitmm_serves(kv_dtype, a.BS, D, a.H, a.Hkv) && a.mode == 1 &&
          a.part_tokens <= kPage * kMaxPages;
 }
 
@@ -436,38 +503,44 @@ bool bf16mm_applies(const RowAttnArgs& a, int kv_dtype, int D) {
 // tokens, and groups of at most 4 query heads (the least arithmetic per
 // byte) share a 512-token partition between 4 waves, so a quarter of the
 // partition states reach HBM.  Measured on C2's batch and contexts, 32 query
-// heads (step, µs, waves x partition tokens):
+// heads, bf16 (step, us, waves x partition tokens):
 //   G = 2:  226 (1 x 256)  217 (2 x 512)  213 (4 x 512)
 //   G = 4:  129 (1 x 256)  126 (2 x 512)  123 (4 x 512)
 //   G = 8:   80 (1 x 256)   77 (2 x 256)   78 (4 x 256)
 //   G = 16:  52 (1 x 128)   50 (2 x 256)   53 (4 x 256)
 //   G = 32:  51 (1 x 128)   49 (2 x 256)   53 (4 x 256)
-int bf16mm_waves(int G) { return G <= 4 ? 4 : 2; }
-int bf16mm_default_partition(int G) { return G <= 4 ? 512 : 256; }
+int splitmm_waves(int G) { return G <= 4 ? 4 : 2; }
+int splitmm_default_partition(int G) { return G <= 4 ? 512 : 256; }
 
-int64_t bf16mm_grid(const RowAttnArgs& a) {
+int64_t splitmm_grid(const RowAttnArgs& a) {
   const int G = a.H / a.Hkv;
   return sat_mul(a.rows, a.P, a.Hkv, ceil_div(G, kSlots));
 }
 
-template <int D, int kW>
+template <typename Ops, int D, int kW>
 static void launch_waves(const RowAttnArgs& a, hipStream_t stream) {
-  const dim3 grid((unsigned)bf16mm_grid(a)), block(64 * kW);
+  const dim3 grid((unsigned)splitmm_grid(a)), block(64 * kW);
   if (a.H / a.Hkv <= 8)   // one head chunk of at most 8 heads: hi/lo as columns
-    hipLaunchKernelGGL((bf16mm_part_kernel<D, true, kW>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((splitmm_part_kernel<Ops, D, true, kW>), grid, block, 0, stream, a);
   else
-    hipLaunchKernelGGL((bf16mm_part_kernel<D, false, kW>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((splitmm_part_kernel<Ops, D, false, kW>), grid, block, 0, stream, a);
 }
 
-void launch_bf16mm_part(const RowAttnArgs& a, int D, hipStream_t stream) {
-  const bool four = bf16mm_waves(a.H / a.Hkv) == 4;
+template <typename Ops>
+static void launch_for(const RowAttnArgs& a, int D, hipStream_t stream) {
+  const bool four = splitmm_waves(a.H / a.Hkv) == 4;
   if (D == 64) {
-    if (four) launch_waves<64, 4>(a, stream);
-    else launch_waves<64, 2>(a, stream);
+    if (four) launch_waves<Ops, 64, 4>(a, stream);
+    else launch_waves<Ops, 64, 2>(a, stream);
   } else {
-    if (four) launch_waves<128, 4>(a, stream);
-    else launch_waves<128, 2>(a, stream);
+    if (four) launch_waves<Ops, 128, 4>(a, stream);
+    else launch_waves<Ops, 128, 2>(a, stream);
   }
+}
+
+void launch_splitmm_part(const RowAttnArgs& a, int kv_dtype, int D, hipStream_t stream) {
+  if (kv_dtype == HS_DTYPE_F16) launch_for<F16Ops>(a, D, stream);
+  else launch_for<Bf16Ops>(a, D, stream);
 }
 
 }  // namespace hs

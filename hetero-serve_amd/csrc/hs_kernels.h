@@ -108,14 +108,14 @@ bool gqa_mfma_applies(const RowAttnArgs& a, int kv_dtype, int D);
 int64_t gqa_mfma_grid(const RowAttnArgs& a);
 void launch_gqa_mfma_part(const RowAttnArgs& a, int kv_dtype, int D, hipStream_t stream);
 
-// Grouped-query decode of bf16 caches on the matrix cores with split bf16
-// operands (hs_decode_bf16mm.hip): fp32-grade results, no conversion.
-bool bf16mm_serves(int kv_dtype, int BS, int D, int H, int Hkv);   // geometry and dtype
-bool bf16mm_applies(const RowAttnArgs& a, int kv_dtype, int D);     // ... and this launch
-int bf16mm_waves(int G);                                            // waves per partition
-int bf16mm_default_partition(int G);                                // tokens, before small-grid cuts
-int64_t bf16mm_grid(const RowAttnArgs& a);
-void launch_bf16mm_part(const RowAttnArgs& a, int D, hipStream_t stream);
+// Grouped-query decode of bf16 and fp16 caches on the matrix cores with split
+// 16-bit operands (hs_decode_splitmm.hip): fp32-grade results, no conversion.
+bool splitmm_serves(int kv_dtype, int BS, int D, int H, int Hkv);   // geometry and dtype
+bool splitmm_applies(const RowAttnArgs& a, int kv_dtype, int D);     // ... and this launch
+int splitmm_waves(int G);                                            // waves per partition
+int splitmm_default_partition(int G);                                // tokens, before small-grid cuts
+int64_t splitmm_grid(const RowAttnArgs& a);
+void launch_splitmm_part(const RowAttnArgs& a, int kv_dtype, int D, hipStream_t stream);
 
 // Query heads one decode wave serves (GQA packing): 1, 2, 4 or 8.
 int row_attn_heads_per_wave(int H, int Hkv);

@@ -119,8 +119,9 @@ size_t hs_decode_workspace_bytes(int B, int H, int Hkv, int D, int BS, int MB, i
  *                     plus the merge (the fast default)
  *   partition_tokens  used when num_splits == 0; 0 = library default (512
  *                tokens, fewer for GQA groups and for grids of fewer than 4
- *                waves per CU; bf16 caches with 2 or more query heads per KV
- *                head: 512 tokens up to 4 heads per KV head, 256 above).
+ *                waves per CU; fp16 and bf16 caches with 2 or more query
+ *                heads per KV head, head dim 64 or 128: 512 tokens up to 4
+ *                heads per KV head, 256 above).
  *                Must be a multiple of 16.
  *   workspace    device scratch of hs_decode_workspace_bytes(...) bytes
  *                (may be NULL when that is 0).
@@ -159,7 +160,7 @@ int hs_decode_noalloc(const float* q, const void* k_cache, const void* v_cache, 
  * partition_tokens keys that is full in at least 4 sequences with identical
  * block ids is read once for up to 32 (sequence, head) query slots of a KV
  * head on the matrix cores (fp16 operands, fp32 accumulation: within 1e-3 of
- * the fp32 path, like the grouped-query matrix-core decode); every other
+ * the fp32 path); every other
  * partition runs as in hs_decode.  The grouping is found on the device by
  * one small kernel per call.  Serves fp16/bf16 KV with BS == 16, D in
  * {32, 64, 128}, partitions of at most 1024 tokens, at most 16 query heads per

@@ -310,6 +310,14 @@ def test_gqa_matrix_core_table_edges():
     assert _maxerr(got[[0, 1]], want[[0, 1]]) <= 2e-3
 
 
+# Split-operand matrix-core decode: hi + lo terms of the cache's type for q
+# and the probabilities; fp32-grade results.  Tolerances (max-abs, O(1)
+# outputs): bf16 5e-5 (hi + lo carry 16 significant bits), fp16 1e-5 (22
+# bits); the fp16-operand path gets 2e-3.
+SPLIT_TOL = {torch.bfloat16: 5e-5, torch.float16: 1e-5}
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("H,Hkv,D", [
     (4, 2, 128),     # G = 2, MFMA columns: hi/lo pairs of 2 heads
     (12, 4, 64),     # G = 3: odd group, columns 3..7 and 11..15 idle
@@ -318,43 +326,44 @@ def test_gqa_matrix_core_table_edges():
     (24, 2, 64),     # G = 12: hi and lo as two products
     (48, 2, 128),    # G = 24: a chunk of 16 heads and one of 8
 ])
-def test_bf16_split_operand_decode(H, Hkv, D):
-    """Grouped-query decode of a bf16 cache runs on the matrix cores with q and
-    the probabilities split into hi + lo bf16 terms: fp32-grade results
-    (5e-5 here, against 2e-3 for the fp16-operand path) for every group size
-    and both column layouts, on partitions from one page to 1024 tokens."""
+def test_split_operand_decode(H, Hkv, D, dtype):
+    """Grouped-query decode of a bf16 or fp16 cache runs on the matrix cores
+    with q and the probabilities split into hi + lo terms of the cache's
+    type: fp32-grade results for every group size and both column layouts,
+    on partitions from one page to 1024 tokens."""
     from heteroserve import _hip
 
     lens = [1, 15, 16, 17, 100, 511, 513, 2000]
-    pool, q, bt, ctx = _random_case(lens, H, Hkv, D, 16, torch.bfloat16, seed=H + 3 * Hkv + D)
+    pool, q, bt, ctx = _random_case(lens, H, Hkv, D, 16, dtype, seed=H + 3 * Hkv + D)
     kp, vp = pool[0, 0], pool[0, 1]
     scale = D ** -0.5
     want = _oracle(q, kp, vp, bt, ctx, scale)
     for p in (16, 128, 1024):
         got = _hip.decode(q, kp, vp, bt, ctx, scale, 0, partition_tokens=p)
-        assert _maxerr(got, want) <= 5e-5, (H, Hkv, D, p)
+        assert _maxerr(got, want) <= SPLIT_TOL[dtype], (H, Hkv, D, p)
 
 
-def test_bf16_split_operand_decode_fuzz():
-    """Seeded random group sizes (2..32 query heads per KV head, odd ones
-    included), head dims, batch shapes and partition lengths for the split-bf16
-    matrix-core decode, each against the oracle at 5e-5."""
+def test_split_operand_decode_fuzz():
+    """Seeded random cache types, group sizes (2..32 query heads per KV head,
+    odd ones included), head dims, batch shapes and partition lengths for the
+    split-operand matrix-core decode, each against the oracle."""
     from heteroserve import _hip
 
     rng = np.random.default_rng(2024)
     groups = [(4, 2), (6, 3), (8, 2), (12, 4), (15, 3), (20, 4), (24, 3), (32, 8), (40, 5),
               (48, 3), (64, 4), (64, 2)]
-    for case in range(16):
+    for case in range(24):
         H, Hkv = groups[case % len(groups)]
+        dtype = (torch.bfloat16, torch.float16)[case % 2]
         D = int(rng.choice([64, 128]))
         lens = [int(x) for x in rng.integers(1, 1500, size=int(rng.integers(1, 7)))]
         pt = int(rng.choice([0, 16, 48, 256, 1024]))
-        pool, q, bt, ctx = _random_case(lens, H, Hkv, D, 16, torch.bfloat16, seed=100 + case)
+        pool, q, bt, ctx = _random_case(lens, H, Hkv, D, 16, dtype, seed=100 + case)
         kp, vp = pool[0, 0], pool[0, 1]
         scale = D ** -0.5
         got = _hip.decode(q, kp, vp, bt, ctx, scale, 0, partition_tokens=pt)
         want = _oracle(q, kp, vp, bt, ctx, scale)
-        assert _maxerr(got, want) <= 5e-5, (case, H, Hkv, D, lens, pt)
+        assert _maxerr(got, want) <= SPLIT_TOL[dtype], (case, dtype, H, Hkv, D, lens, pt)
 
 
 def test_errors_are_raised_with_reference_messages():

@@ -53,10 +53,14 @@ def test_decode_prefill_and_pack_replay_bit_exact():
     dec = build_decode("g", np.array([1, 300, 1100, 4000, 17]), 8, 8, 128, 800,
                        torch.bfloat16, DEV, seed=12)
     dec_args = (dec.q, dec.k_cache, dec.v_cache, dec.block_tables, dec.context_lens, dec.scale)
-    # grouped-query decode of a bf16 cache: the split-bf16 matrix-core kernel
+    # grouped-query decode of a bf16 and of an fp16 cache: the split-operand
+    # matrix-core kernel (with its power-of-two query scaling for fp16)
     gqa = build_decode("g", np.array([5, 700, 2500, 16]), 32, 8, 128, 300,
                        torch.bfloat16, DEV, seed=14)
     gqa_args = (gqa.q, gqa.k_cache, gqa.v_cache, gqa.block_tables, gqa.context_lens, gqa.scale)
+    g16 = build_decode("g", np.array([900, 3, 1800]), 16, 8, 64, 200, torch.float16, DEV,
+                       seed=15)
+    g16_args = (g16.q, g16.k_cache, g16.v_cache, g16.block_tables, g16.context_lens, g16.scale)
     # a single chunk: a small grid, so the MFMA prefill splits the key range
     # and runs its merge kernel too
     pre = build_prefill("g", np.array([700]), np.array([300]), 8, 8, 128, 80,
@@ -70,6 +74,7 @@ def test_decode_prefill_and_pack_replay_bit_exact():
 
     want_dec = paged_attn.paged_attention(*dec_args)
     want_gqa = paged_attn.paged_attention(*gqa_args)
+    want_g16 = paged_attn.paged_attention(*g16_args)
     want_pre = paged_attn_wmma.paged_attention_prefill_wmma(*pre_args)
     _hip.kv_pack(pool, ids, packed)
     want_pack = packed.clone()
@@ -78,9 +83,11 @@ def test_decode_prefill_and_pack_replay_bit_exact():
     def step():
         d = paged_attn.paged_attention(*dec_args)
         g = paged_attn.paged_attention(*gqa_args)
+        h = paged_attn.paged_attention(*g16_args)
         p = paged_attn_wmma.paged_attention_prefill_wmma(*pre_args)
         _hip.kv_pack(pool, ids, packed)
-        return d, g, p
+        return d, g, h, p
 
-    graph, (d, g, p) = _capture(step)
-    _replays_match(graph, [d, g, p, packed], [want_dec, want_gqa, want_pre, want_pack])
+    graph, (d, g, h, p) = _capture(step)
+    _replays_match(graph, [d, g, h, p, packed],
+                   [want_dec, want_gqa, want_g16, want_pre, want_pack])

@@ -7,7 +7,9 @@ once scaled.  The reference never meets this: its WMMA path admits fp16
 caches only (paged_attn_wmma.py:266-267, :372-387) and its torch oracle
 computes in fp32 (paged_attn.py:255-298, paged_attn_prefill.py:281-322).
 Here each kernel checks the operands it converts and recomputes an affected
-unit in fp32, so the result must match the fp32 oracle.
+unit in fp32, so the result must match the fp32 oracle.  The split-operand
+decode (16-bit caches, 2+ query heads per KV head) converts nothing from the
+cache and scales the query into range, so it needs no such fallback.
 
 Tolerance, per element: 2e-3 * max(1, |oracle|) -- the north-star 2e-3
 max-abs where outputs are O(1), 2e-3 relative where a planted V value makes
@@ -226,6 +228,53 @@ def test_gqa_decode_operands_beyond_fp16(target, H, Hkv, D):
     for b in range(len(lens)):
         _assert_close(got[b], _decode_oracle(q, kc, vc, bt, lens, scale, b),
                       f"{target} H{H}/{Hkv} D{D} seq {b}")
+
+
+# ---------------------------------------------------------------------------
+# split-operand matrix-core decode (splitmm_part_kernel)
+# ---------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("H,Hkv,D", [(8, 4, 128), (32, 4, 128), (48, 2, 64)])
+def test_split_decode_query_and_cache_range(H, Hkv, D, dtype):
+    """2 to 24 query heads per KV head on 16-bit caches (the split-operand
+    decode, no fallback): heads scaled by 1e-30 .. 1e20 -- far outside fp16
+    either way once multiplied by scale * log2(e) -- side by side in one KV
+    group, and cache values up to 6e4 in K and V.  For fp16 each head's query
+    is brought into range by a power of two before it is split, so every
+    sequence must match the fp32 oracle to 2e-5 * max(1, |oracle|) (fp16) or
+    5e-5 (bf16), far inside the 2e-3 of the paths above.
+
+    The factors give either near-uniform or one-hot attention.  In between
+    (a factor of 300 puts scores near 400, and two tokens can share the
+    weight) any fp32 evaluation is off by some 1e-5: measured on such a head,
+    the fp32 oracle was 4.1e-5 from an fp64 evaluation and this kernel
+    2.2e-5, so such heads would test the oracle's rounding, not the kernel."""
+    from heteroserve import _hip
+    from heteroserve.model import paged_attn
+
+    lens = [40, 511, 700, 1500, 3000]
+    rng, tables, kc, vc, q = _decode_case(lens, H, Hkv, D, dtype, seed=H + D + 7)
+    factors = [1.0, 1e6, 1e-7, 1e-30, 1e20, 0.01]
+    for h in range(H):
+        q[:, h] *= factors[h % len(factors)]
+    for cache in (kc, vc):
+        for b, t in [(1, 77), (3, 1000), (4, 2999)]:
+            cache[tables[b][t // BS], t % BS, int(rng.integers(Hkv)), int(rng.integers(D))] = \
+                float(rng.choice([6e4, -6e4]))
+    bt = _table_tensor(tables)
+    ctx = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    scale = D ** -0.5
+    tol = 2e-5 if dtype == torch.float16 else 5e-5
+    for pt in (0, 16, 1024):
+        got = _hip.decode(q, kc, vc, bt, ctx, scale, 0, partition_tokens=pt).cpu()
+        assert torch.isfinite(got).all()
+        for b in range(len(lens)):
+            want = _decode_oracle(q, kc, vc, bt, lens, scale, b)
+            err = (got[b] - want).abs() / torch.clamp(want.abs(), min=1.0)
+            assert err.max().item() <= tol, (dtype, H, Hkv, D, pt, b, err.max().item())
+    assert torch.isfinite(paged_attn.paged_attention(q, kc, vc, bt, ctx, scale)).all()
 
 
 # ---------------------------------------------------------------------------
