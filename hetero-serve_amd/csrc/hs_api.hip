@@ -121,7 +121,7 @@ static int default_partition(int B, int H, int Hkv, int BS, int MB, int kv_dtype
   if (splitmm_serves(kv_dtype, BS, D, H, Hkv)) {
     // split-operand matrix-core decode: splitmm_waves(G) waves share a partition
     const int kw = splitmm_waves(G);
-    return shrink_for_small_grid(splitmm_default_partition(G),
+    return shrink_for_small_grid(splitmm_default_partition(G, D),
                                  std::max(kMinDefaultPartition, BS * kw),
                                  sat_mul(B, Hkv, ceil_div(G, 16), kw), BS, MB);
   }

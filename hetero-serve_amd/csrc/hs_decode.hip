@@ -206,10 +206,9 @@ static int launch_dim(const RowAttnArgs& a, int D, hipStream_t stream) {
 }
 
 // Launch the partition kernel (+ merge when P > 1).  Arguments are validated
-// by the caller.  Grouped-query calls on 16-bit caches go to the matrix
-// cores: the split-operand kernel (hs_decode_splitmm.hip) where it serves,
-// else the fp16-operand kernel (hs_decode_gqa.hip, head_dim 32); the rest run
-// the VALU kernel above.  With
+// by the caller.  Grouped-query calls on 16-bit caches with 16-token pages
+// and fixed partitions go to the split-operand matrix-core kernel
+// (hs_decode_splitmm.hip); the rest run the VALU kernel above.  With
 // `shared`: the plan kernel, then the shared-page kernel, then the partition
 // kernel (which skips the grouped partitions), then the merge.  The shared
 // kernel runs first, alone: beside the partition kernel its large workgroups
@@ -217,12 +216,9 @@ static int launch_dim(const RowAttnArgs& a, int D, hipStream_t stream) {
 int launch_row_attn(const RowAttnArgs& a, int kv_dtype, int D, hipStream_t stream,
                     const SharePlanArgs* shared) {
   const bool splitmm = splitmm_applies(a, kv_dtype, D);
-  const bool mfma = !splitmm && gqa_mfma_applies(a, kv_dtype, D);
   int64_t gx;
   if (splitmm) {
     gx = splitmm_grid(a);
-  } else if (mfma) {
-    gx = gqa_mfma_grid(a);
   } else {
     const int G = row_attn_heads_per_wave(a.H, a.Hkv);
     gx = sat_mul(a.rows, a.P, ceil_div(a.H / G, kDecodeWaves));
@@ -242,10 +238,6 @@ int launch_row_attn(const RowAttnArgs& a, int kv_dtype, int D, hipStream_t strea
   if (splitmm) {
     profile_begin(stream);
     launch_splitmm_part(a, kv_dtype, D, stream);
-    profile_end(stream);
-  } else if (mfma) {
-    profile_begin(stream);
-    launch_gqa_mfma_part(a, kv_dtype, D, stream);
     profile_end(stream);
   } else if (kv_dtype == HS_DTYPE_F32) {
     rc = launch_dim<float>(a, D, stream);

@@ -1,17 +1,18 @@
-// Grouped-query decode on gfx950 matrix cores.
+// Shared pages (prefix caching) on gfx950 matrix cores.
 //
 // Reference: paged_attn_v2.py:75-157 (one query row per head, KV head
 // h / (H / Hkv), online softmax) and paged_attn_v3.py:75-208 (partitions
-// merged by log-sum-exp).  When G = H / Hkv query heads share a KV head, the
-// per-token work of the VALU kernel (hs_decode.hip) grows with G while the
-// bytes read stay the same; here it goes to the matrix cores instead.
+// merged by log-sum-exp).  Sequences whose partition has the same block ids
+// (a shared prefix) read the same K/V; share_plan_kernel finds such groups on
+// the device, and shared_pages_kernel reads each grouped partition once for
+// up to 32 query slots, (sequence, head) pairs of one KV head.  There is no
+// reference counterpart (the reference reads every sequence's pages).
 //
-// One wave serves up to 32 query heads of one KV group for one (row,
-// partition) and walks the partition in blocks of 32 tokens:
+// The wave code (gqa_wave_run) walks a partition in blocks of 32 tokens:
 //   S^T = K . Q^T   v_mfma_f32_32x32x16_f16, K rows (tokens) the A operand,
-//                   Q^T (heads) the B operand, held in registers;
+//                   Q^T (query slots) the B operand, held in registers;
 //   O^T += V^T . P^T  the accumulator of the first product is already the B
-//                   operand layout of the second (lane = head), so P stays in
+//                   operand layout of the second (lane = slot), so P stays in
 //                   registers.
 // K and V are loaded with 16 lanes per 256-byte token row (loading K straight
 // into the operand layout, one token per lane, touched 32 rows per load
@@ -22,30 +23,20 @@
 // to be tokens 8h..8h+7 of a 16-token chunk; the two differ by a swap of bits
 // 2 and 3 of the token index, so K's LDS row r holds token swap23(r).
 //
-// Operands are fp16 (bf16 KV is widened exactly for |x| < 65504; fp32 KV
-// keeps the VALU kernel), scores and the softmax state are fp32 in base 2
-// (scale * log2(e) folded into q), and the running max is raised lazily (only
-// when a block's max exceeds it by more than 8), as in the MFMA prefill.
-// The partition states (m, l, un-normalised acc) have the layout and meaning
-// of the VALU kernel's, so the same merge kernel combines them.
+// Operands are fp16 (bf16 KV is widened exactly for |x| < 65504), scores and
+// the softmax state are fp32 in base 2 (scale * log2(e) folded into q), and
+// the running max is raised lazily (only when a block's max exceeds it by
+// more than 8), as in the MFMA prefill.  A group whose operands fp16 cannot
+// hold is handed back to the partition kernel.  The partition states (m, l,
+// un-normalised acc) have the layout and meaning of the VALU kernel's, so the
+// same merge kernel combines them.
 //
-// The same wave code serves shared pages (prefix caching, hs_decode_shared):
-// there the 32 query slots of a wave are (sequence, head) pairs of several
-// sequences whose partition has the same block ids, found on the device by
-// share_plan_kernel, so such a partition is read once for all of them.
-//
-// Used for paged caches with 16-token blocks, fixed partitions of at most
-// 1024 tokens, head_dim 32, 64 or 128 and at least 8 query heads per KV
-// head (at 4 the VALU kernel's packed heads measured faster: 169 against
-// 197 us on C2's geometry with 8 KV heads); every other case runs the VALU
-// kernel.  A partition's block ids (at
-// most 64 pages) are fetched once by one vector load; every K/V load is
-// unconditional (ids clamped to the table, pages past the end masked), so the
-// compiler's wait counts stay exact, and the next block's loads are in flight
-// while the current block is computed.
+// A partition's block ids (at most 64 pages) are fetched once by one vector
+// load; every K/V load is unconditional (ids clamped to the table, pages past
+// the end masked), so the compiler's wait counts stay exact, and the next
+// block's loads are in flight while the current block is computed.
 #include "hs_kernels.h"
 #include "hs_mfma.h"
-#include "hs_rowwalk.h"
 
 namespace hs {
 
@@ -255,36 +246,6 @@ __device__ inline bool gqa_wave_run(const RowAttnArgs& a, GqaWaveLds<D>& w, int 
   return __builtin_amdgcn_ballot_w64(f16_check_failed(chk)) != 0;
 }
 
-// fp32 recomputation of a wave's unit (RowWalk, the VALU decode arithmetic):
-// query heads h0 .. h0 + gc - 1 of KV head kvh for keys [lo, hi) of `row`,
-// written as the matrix-core pass would have (normalised output when the
-// partition is the row's only one, else partition states).  One head per
-// walk: a walk of eight would need more registers than the matrix-core pass
-// and lower the kernel's occupancy (measured: 101 -> 227 VGPRs at head dim 32).
-template <typename T, int D, int G>
-__device__ inline void walk_heads_fp32(const RowAttnArgs& a, int kvh, int h0, const int32_t* bt,
-                                       int lo, int hi, int row, int p, bool direct) {
-  RowWalk<T, D, true, G> w;   // 16-token pages: a load group never straddles one
-  const int64_t orow0 = ((int64_t)row * a.H + h0) * D;
-  w.run(KvPages{a.k, a.v, a.Hkv, a.BS, a.NB}, a.q + orow0, a.qscale, kvh, bt, lo, hi);
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    if (direct) {
-      w.store_out(g, a.out + orow0 + g * D);
-    } else {
-      const int64_t pi = ((int64_t)row * a.H + h0 + g) * a.P + p;
-      w.store_state(g, a.part_acc + pi * D, reinterpret_cast<float2*>(a.part_ml) + pi);
-    }
-  }
-}
-
-template <typename T, int D>
-__device__ inline void gqa_unit_fp32(const RowAttnArgs& a, int kvh, int h0, int gc,
-                                     const int32_t* bt, int lo, int hi, int row, int p,
-                                     bool direct) {
-  for (int g = 0; g < gc; ++g) walk_heads_fp32<T, D, 1>(a, kvh, h0 + g, bt, lo, hi, row, p, direct);
-}
-
 // Result of slot j of a wave: lane (j, hh) owns dims d*32 + 8g + 4hh + 0..3.
 template <int D>
 __device__ inline void gqa_wave_store(const RowAttnArgs& a, int lane, int gc,
@@ -317,66 +278,6 @@ __device__ inline void gqa_wave_store(const RowAttnArgs& a, int lane, int gc,
   }
 }
 
-
-template <typename T, int D>
-__global__ __launch_bounds__(kGqaWaves * 64) __attribute__((amdgpu_waves_per_eu(2)))
-void gqa_mfma_part_kernel(RowAttnArgs a) {
-  __shared__ GqaWaveLds<D> lds[kGqaWaves];
-  const int lane = threadIdx.x & 63;
-  const int wv = threadIdx.x >> 6;
-  const int j = lane & 31;
-  const int G = a.H / a.Hkv;
-  const int n_hc = (G + kHeadsPerWave - 1) / kHeadsPerWave;   // head chunks per KV head
-  const int n_units = a.Hkv * n_hc;
-  // Waves are numbered unit-fastest over (row, partition, unit), so the waves
-  // of a workgroup read neighbouring KV heads of the same tokens, and take
-  // further (row, partition) pairs when a row has fewer than kGqaWaves units.
-  const int64_t gw = (int64_t)blockIdx.x * kGqaWaves + wv;
-  if (gw >= (int64_t)a.rows * a.P * n_units) return;   // no barriers below
-  const int unit = (int)(gw % n_units);
-  const int kvh = unit / n_hc;
-  const int hc = unit - kvh * n_hc;
-  const int h0 = kvh * G + hc * kHeadsPerWave;
-  const int gc = min(kHeadsPerWave, G - hc * kHeadsPerWave);   // heads of this wave
-  const int64_t rp = gw / n_units;
-  const int row = (int)(rp / a.P);
-  const int p = (int)(rp - (int64_t)row * a.P);
-  if (a.skip && a.skip[rp]) return;   // served by the shared-page kernel
-
-  int b, end;
-  if (!row_geometry(a, row, b, end)) return;
-  int lo = 0, hi = 0, nparts = 0;
-  const bool live = partition_range(a, end, p, lo, hi, nparts);
-  const int64_t orow0 = ((int64_t)row * a.H + h0) * D;
-  if (!live) {
-    if (end <= 0 && p == 0) {   // nothing to attend to: zero rows
-      for (int d = lane; d < gc * D; d += 64) a.out[orow0 + d] = 0.0f;
-    }
-    return;
-  }
-  const int32_t* bt = a.bt + (int64_t)b * a.MB;
-  float16x o[D / 32];
-  float m, l;
-  if (gqa_wave_run<T, D>(a, lds[wv], lane, kvh, gc, bt, lo, hi,
-                         orow0 + (int64_t)min(j, gc - 1) * D, o, m, l)) {
-    gqa_unit_fp32<T, D>(a, kvh, h0, gc, bt, lo, hi, row, p, nparts == 1);
-    return;
-  }
-  gqa_wave_store<D>(a, lane, gc, o, m, l, nparts == 1, orow0 + (int64_t)j * D,
-                    ((int64_t)row * a.H + h0 + j) * a.P + p);
-}
-
-int64_t grid_size(const RowAttnArgs& a) {
-  const int G = a.H / a.Hkv;
-  const int64_t waves = sat_mul(a.rows, a.P, a.Hkv, ceil_div(G, kHeadsPerWave));
-  return ceil_div(waves, kGqaWaves);
-}
-
-template <typename T, int D>
-void launch_typed(const RowAttnArgs& a, hipStream_t stream) {
-  hipLaunchKernelGGL((gqa_mfma_part_kernel<T, D>), dim3((unsigned)grid_size(a)),
-                     dim3(kGqaWaves * 64), 0, stream, a);
-}
 
 // ---------------------------------------------------------------------------
 // Shared pages (prefix caching): sequences whose full partition p has the
@@ -664,14 +565,6 @@ void shared_pages_kernel(RowAttnArgs a, SharePlanArgs s) {
 
 }  // namespace
 
-bool gqa_mfma_applies(const RowAttnArgs& a, int kv_dtype, int D) {
-  return (kv_dtype == HS_DTYPE_F16 || kv_dtype == HS_DTYPE_BF16) && a.BS == 16 &&
-         (D == 32 || D == 64 || D == 128) && a.H / a.Hkv >= 8 && a.mode == 1 &&
-         a.part_tokens <= 1024;
-}
-
-int64_t gqa_mfma_grid(const RowAttnArgs& a) { return grid_size(a); }
-
 bool shared_pages_apply(const RowAttnArgs& a, int kv_dtype, int D) {
   const int G = a.H / a.Hkv;
   return (kv_dtype == HS_DTYPE_F16 || kv_dtype == HS_DTYPE_BF16) && a.BS == 16 &&
@@ -704,22 +597,6 @@ void launch_shared_pages(const RowAttnArgs& a, const SharePlanArgs& s, int kv_dt
       case 32: hipLaunchKernelGGL((shared_pages_kernel<Bf16, 32>), grid, block, 0, stream, a, s); break;
       case 64: hipLaunchKernelGGL((shared_pages_kernel<Bf16, 64>), grid, block, 0, stream, a, s); break;
       default: hipLaunchKernelGGL((shared_pages_kernel<Bf16, 128>), grid, block, 0, stream, a, s); break;
-    }
-  }
-}
-
-void launch_gqa_mfma_part(const RowAttnArgs& a, int kv_dtype, int D, hipStream_t stream) {
-  if (kv_dtype == HS_DTYPE_F16) {
-    switch (D) {
-      case 32: launch_typed<_Float16, 32>(a, stream); break;
-      case 64: launch_typed<_Float16, 64>(a, stream); break;
-      default: launch_typed<_Float16, 128>(a, stream); break;
-    }
-  } else {
-    switch (D) {
-      case 32: launch_typed<Bf16, 32>(a, stream); break;
-      case 64: launch_typed<Bf16, 64>(a, stream); break;
-      default: launch_typed<Bf16, 128>(a, stream); break;
     }
   }
 }

@@ -15,8 +15,9 @@
 // instructions per page instead.  Measured on MI355X, C2's batch and contexts
 // with 32 query heads (whole decode call, bf16, D = 128): 2 / 4 / 8 / 16 / 32
 // heads per KV head 217 / 124 / 78 / 51 / 50 us, against 232 / 148 us for
-// the VALU kernel and 125 / 95 / 64 us for the fp16-operand matrix-core
-// kernel (hs_decode_gqa.hip), which now serves only head_dim 32.
+// the VALU kernel and 125 / 95 / 64 us for an fp16-operand matrix-core kernel
+// (q and the probabilities rounded to fp16, ~1e-3 error) that this one
+// replaced.
 //
 // Numerics.  K and V go to the MFMAs as they are stored (no conversion).  The
 // query and the probabilities are fp32; each is split into two terms of the
@@ -87,8 +88,11 @@ constexpr int kMaxPages = 64;      // pages of a partition: one block id per lan
 
 // One page of K and of V, both token-major as in the cache.  Row paddings:
 // K rows are read as 16-byte MFMA fragments (row j by lane j), V rows by the
-// transposing read below (four rows by each group of 16 lanes); the pads make
-// both conflict-free at D = 128 and keep the 16-byte row stores whole.
+// transposing read below (four rows by each group of 16 lanes).  With K rows
+// of D + 8 and V rows of D + 16 halves, the 16 lanes of a group land on
+// disjoint banks at D = 32, 64 and 128 (K: 16 spans of 4 banks at stride
+// (D + 8) / 2 dwords; V: 4 rows x 4 pairs at stride (D + 16) / 2), and the
+// 16-byte row stores stay whole.
 template <int D>
 struct PageLds {
   static constexpr int kKRow = D + 8;
@@ -491,7 +495,7 @@ __global__ __launch_bounds__(64 * kW) void splitmm_part_kernel(RowAttnArgs a) {
 
 bool splitmm_serves(int kv_dtype, int BS, int D, int H, int Hkv) {
   return (kv_dtype == HS_DTYPE_BF16 || kv_dtype == HS_DTYPE_F16) && BS == kPage &&
-         (D == 64 || D == 128) && H / Hkv >= 2;
+         (D == 32 || D == 64 || D == 128) && H / Hkv >= 2;
 }
 
 bool splitmm_applies(const RowAttnArgs& a, int kv_dtype, int D) {
@@ -509,8 +513,10 @@ bool splitmm_applies(const RowAttnArgs& a, int kv_dtype, int D) {
 //   G = 8:   80 (1 x 256)   77 (2 x 256)   78 (4 x 256)
 //   G = 16:  52 (1 x 128)   50 (2 x 256)   53 (4 x 256)
 //   G = 32:  51 (1 x 128)   49 (2 x 256)   53 (4 x 256)
+// At head dim 32 (1-KB head pages) 256 tokens measured best or within 4% for
+// every G (C2 contexts, fp16, 32 query heads: G = 2 / 4 / 8: 119 / 65 / 40 us).
 int splitmm_waves(int G) { return G <= 4 ? 4 : 2; }
-int splitmm_default_partition(int G) { return G <= 4 ? 512 : 256; }
+int splitmm_default_partition(int G, int D) { return D == 32 || G > 4 ? 256 : 512; }
 
 int64_t splitmm_grid(const RowAttnArgs& a) {
   const int G = a.H / a.Hkv;
@@ -529,7 +535,10 @@ static void launch_waves(const RowAttnArgs& a, hipStream_t stream) {
 template <typename Ops>
 static void launch_for(const RowAttnArgs& a, int D, hipStream_t stream) {
   const bool four = splitmm_waves(a.H / a.Hkv) == 4;
-  if (D == 64) {
+  if (D == 32) {
+    if (four) launch_waves<Ops, 32, 4>(a, stream);
+    else launch_waves<Ops, 32, 2>(a, stream);
+  } else if (D == 64) {
     if (four) launch_waves<Ops, 64, 4>(a, stream);
     else launch_waves<Ops, 64, 2>(a, stream);
   } else {

@@ -101,19 +101,12 @@ void launch_shared_pages(const RowAttnArgs& a, const SharePlanArgs& s, int kv_dt
 int launch_row_attn(const RowAttnArgs& a, int kv_dtype, int D, hipStream_t stream,
                     const SharePlanArgs* shared = nullptr);
 
-// Grouped-query partition kernel on the matrix cores (hs_decode_gqa.hip):
-// whether it serves this call, its grid size, and its launch (the merge of
-// its partition states is the VALU path's).
-bool gqa_mfma_applies(const RowAttnArgs& a, int kv_dtype, int D);
-int64_t gqa_mfma_grid(const RowAttnArgs& a);
-void launch_gqa_mfma_part(const RowAttnArgs& a, int kv_dtype, int D, hipStream_t stream);
-
 // Grouped-query decode of bf16 and fp16 caches on the matrix cores with split
 // 16-bit operands (hs_decode_splitmm.hip): fp32-grade results, no conversion.
 bool splitmm_serves(int kv_dtype, int BS, int D, int H, int Hkv);   // geometry and dtype
 bool splitmm_applies(const RowAttnArgs& a, int kv_dtype, int D);     // ... and this launch
 int splitmm_waves(int G);                                            // waves per partition
-int splitmm_default_partition(int G);                                // tokens, before small-grid cuts
+int splitmm_default_partition(int G, int D);                         // tokens, before small-grid cuts
 int64_t splitmm_grid(const RowAttnArgs& a);
 void launch_splitmm_part(const RowAttnArgs& a, int kv_dtype, int D, hipStream_t stream);
 

@@ -265,11 +265,11 @@ def test_small_grid_default_partition():
 
 @pytest.mark.parametrize("H,Hkv,D,dtype", [
     (32, 8, 128, torch.bfloat16),   # llama3-8b shape (config.py:85-93), G = 4
-    (32, 1, 128, torch.bfloat16),   # MQA: one wave serves all 32 query heads
-    (40, 1, 128, torch.float16),    # G = 40: two head chunks, the second of 8
+    (32, 1, 128, torch.bfloat16),   # MQA: two head chunks of 16
+    (40, 1, 128, torch.float16),    # G = 40: head chunks of 16, 16 and 8
     (64, 2, 64, torch.bfloat16),    # G = 32 at head_dim 64
     (16, 2, 32, torch.float16),     # G = 8 at head_dim 32
-    (12, 3, 128, torch.bfloat16),   # G = 4, 3 KV heads (not a multiple of 4 waves)
+    (12, 3, 128, torch.bfloat16),   # G = 4, 3 KV heads
 ])
 def test_gqa_matrix_core_decode(H, Hkv, D, dtype):
     """Grouped-query decode on the matrix cores (16-token pages, fixed
@@ -313,7 +313,7 @@ def test_gqa_matrix_core_table_edges():
 # Split-operand matrix-core decode: hi + lo terms of the cache's type for q
 # and the probabilities; fp32-grade results.  Tolerances (max-abs, O(1)
 # outputs): bf16 5e-5 (hi + lo carry 16 significant bits), fp16 1e-5 (22
-# bits); the fp16-operand path gets 2e-3.
+# bits), against the reference tests' 2e-3.
 SPLIT_TOL = {torch.bfloat16: 5e-5, torch.float16: 1e-5}
 
 
@@ -325,6 +325,8 @@ SPLIT_TOL = {torch.bfloat16: 5e-5, torch.float16: 1e-5}
     (32, 4, 128),    # G = 8: all 16 columns in use
     (24, 2, 64),     # G = 12: hi and lo as two products
     (48, 2, 128),    # G = 24: a chunk of 16 heads and one of 8
+    (8, 4, 32),      # head dim 32: one page per load, one QK k-step
+    (40, 1, 32),     # head dim 32, G = 40
 ])
 def test_split_operand_decode(H, Hkv, D, dtype):
     """Grouped-query decode of a bf16 or fp16 cache runs on the matrix cores
@@ -345,8 +347,8 @@ def test_split_operand_decode(H, Hkv, D, dtype):
 
 def test_split_operand_decode_fuzz():
     """Seeded random cache types, group sizes (2..32 query heads per KV head,
-    odd ones included), head dims, batch shapes and partition lengths for the
-    split-operand matrix-core decode, each against the oracle."""
+    odd ones included), head dims (32, 64, 128), batch shapes and partition
+    lengths for the split-operand matrix-core decode, each against the oracle."""
     from heteroserve import _hip
 
     rng = np.random.default_rng(2024)
@@ -355,7 +357,7 @@ def test_split_operand_decode_fuzz():
     for case in range(24):
         H, Hkv = groups[case % len(groups)]
         dtype = (torch.bfloat16, torch.float16)[case % 2]
-        D = int(rng.choice([64, 128]))
+        D = int(rng.choice([32, 64, 128]))
         lens = [int(x) for x in rng.integers(1, 1500, size=int(rng.integers(1, 7)))]
         pt = int(rng.choice([0, 16, 48, 256, 1024]))
         pool, q, bt, ctx = _random_case(lens, H, Hkv, D, 16, dtype, seed=100 + case)

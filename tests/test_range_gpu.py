@@ -1,15 +1,16 @@
 """Operands beyond fp16 range on the matrix-core paths.
 
-The MFMA prefill, the grouped-query matrix-core decode and the shared-page
-decode feed fp16 operands to the matrix cores.  A bf16 cache can hold values
+The MFMA prefill and the shared-page decode feed fp16 operands to the matrix
+cores.  A bf16 cache can hold values
 fp16 cannot (|x| >= 65536 rounds to inf), and a large query overflows fp16
 once scaled.  The reference never meets this: its WMMA path admits fp16
 caches only (paged_attn_wmma.py:266-267, :372-387) and its torch oracle
 computes in fp32 (paged_attn.py:255-298, paged_attn_prefill.py:281-322).
-Here each kernel checks the operands it converts and recomputes an affected
-unit in fp32, so the result must match the fp32 oracle.  The split-operand
-decode (16-bit caches, 2+ query heads per KV head) converts nothing from the
-cache and scales the query into range, so it needs no such fallback.
+Here each such kernel checks the operands it converts and recomputes an
+affected unit in fp32 (the shared-page decode hands it back to the partition
+kernel), so the result must match the fp32 oracle.  The grouped-query decode
+(split operands of the cache's own type, the query scaled into range)
+converts nothing and needs no fallback; its tests here check exactly that.
 
 Tolerance, per element: 2e-3 * max(1, |oracle|) -- the north-star 2e-3
 max-abs where outputs are O(1), 2e-3 relative where a planted V value makes
@@ -184,7 +185,7 @@ def test_prefill_garbage_beyond_the_context():
 
 
 # ---------------------------------------------------------------------------
-# grouped-query decode on the matrix cores (gqa_mfma_part_kernel)
+# grouped-query decode on the matrix cores (splitmm_part_kernel)
 # ---------------------------------------------------------------------------
 
 
@@ -206,10 +207,10 @@ def _decode_oracle(q, kc, vc, bt, lens, scale, b):
 @pytest.mark.parametrize("target", ["K", "V", "KV", "Q"])
 @pytest.mark.parametrize("H,Hkv,D", [(32, 4, 128), (32, 1, 128), (16, 2, 64), (16, 2, 32)])
 def test_gqa_decode_operands_beyond_fp16(target, H, Hkv, D):
-    """8 to 32 query heads per KV head (the matrix-core decode) with planted
-    bf16 values or a 1e6 query: every sequence within tolerance of the fp32
-    oracle, for one-partition rows (direct output) and multi-partition rows
-    (partition states and the merge)."""
+    """8 to 32 query heads per KV head (the matrix-core decode, head dims 32,
+    64 and 128) with planted bf16 values or a 1e6 query: every sequence within
+    tolerance of the fp32 oracle, for one-partition rows (direct output) and
+    multi-partition rows (partition states and the merge)."""
     from heteroserve.model import paged_attn
 
     lens = [40, 511, 700, 1500, 3000]
