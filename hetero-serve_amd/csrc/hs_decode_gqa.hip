@@ -1,4 +1,4 @@
-// Shared pages (prefix caching) on gfx950 matrix cores.
+// Shared pages (prefix caching) on gfx950 matrix cores, at fp32 accuracy.
 //
 // Reference: paged_attn_v2.py:75-157 (one query row per head, KV head
 // h / (H / Hkv), online softmax) and paged_attn_v3.py:75-208 (partitions
@@ -9,27 +9,37 @@
 // reference counterpart (the reference reads every sequence's pages).
 //
 // The wave code (gqa_wave_run) walks a partition in blocks of 32 tokens:
-//   S^T = K . Q^T   v_mfma_f32_32x32x16_f16, K rows (tokens) the A operand,
-//                   Q^T (query slots) the B operand, held in registers;
+//   S^T = K . Q^T   v_mfma_f32_32x32x16_{bf16,f16}, K rows (tokens) the A
+//                   operand, Q^T (query slots) the B operand, held in
+//                   registers;
 //   O^T += V^T . P^T  the accumulator of the first product is already the B
 //                   operand layout of the second (lane = slot), so P stays in
-//                   registers.
+//                   registers; V^T is read from the token-major V rows with
+//                   the transposing LDS read ds_read_b64_tr_b16.
 // K and V are loaded with 16 lanes per 256-byte token row (loading K straight
 // into the operand layout, one token per lane, touched 32 rows per load
-// instruction and measured 4x slower per block) and staged through the
-// wave's own LDS: K row-major, V transposed.
+// instruction and measured 4x slower per block) and staged, as stored,
+// through the wave's own LDS.
 // Token order: the accumulator gives lane half h the token rows 8g + 4h + m
 // in registers 4g + m, while the P.V operand wants registers 0..7 of half h
 // to be tokens 8h..8h+7 of a 16-token chunk; the two differ by a swap of bits
 // 2 and 3 of the token index, so K's LDS row r holds token swap23(r).
 //
-// Operands are fp16 (bf16 KV is widened exactly for |x| < 65504), scores and
-// the softmax state are fp32 in base 2 (scale * log2(e) folded into q), and
-// the running max is raised lazily (only when a block's max exceeds it by
-// more than 8), as in the MFMA prefill.  A group whose operands fp16 cannot
-// hold is handed back to the partition kernel.  The partition states (m, l,
-// un-normalised acc) have the layout and meaning of the VALU kernel's, so the
-// same merge kernel combines them.
+// Numerics: split operands, as in the grouped-query decode
+// (hs_decode_splitmm.hip).  K and V go to the MFMAs as stored; the query and
+// the probabilities are fp32, each split into two terms of the cache's type
+// (x = hi + lo, hi = T(x), lo = T(x - hi)), and every product is taken
+// against both terms.  Products of 16-bit values are exact in the fp32
+// accumulators, so scores and outputs match fp32 arithmetic to about 2^-16
+// relative (bf16) or better (fp16), and no input value needs a fallback.  For
+// fp16 caches each slot's scaled query is first multiplied by a power of two
+// that puts its largest element in [2^14, 2^15) (the scores are multiplied
+// back, exactly), and the probabilities are taken 2^7 larger: neither term
+// overflows fp16.  Scores and the softmax state are fp32 in base 2
+// (scale * log2(e) folded into q), and the running max is raised lazily
+// (only when a block's max exceeds it by more than 8), as in the MFMA
+// prefill.  The partition states (m, l, un-normalised acc) have the layout
+// and meaning of the VALU kernel's, so the same merge kernel combines them.
 //
 // A partition's block ids (at most 64 pages) are fetched once by one vector
 // load; every K/V load is unconditional (ids clamped to the table, pages past
@@ -47,47 +57,95 @@ using namespace mfma;
 constexpr int kGqaWaves = 4;        // waves per workgroup: consecutive head units
 constexpr int kHeadsPerWave = 32;   // MFMA N dimension
 constexpr int kBlock = 32;          // tokens per block
-constexpr int kVtPad = 8;           // halves of padding per V^T row
 constexpr float kSlack = 8.0f;      // lazy-rescale slack, log2 units
 
-constexpr int kKPad = 8;            // halves of padding per K row
+constexpr int kKPad = 8;            // 16-bit words of padding per K row
+// Padding per V row: a transposing read of V^T fragments has each 32-lane
+// half of the wave read 4 rows x 64 bytes (two 16-lane groups, adjacent
+// 16-dim column blocks); a row stride of 16 or 48 dwords mod 64 puts those 4
+// rows on disjoint 16-bank ranges.
+template <int D>
+constexpr int v_pad() { return D == 32 ? 0 : 32; }
 
+// One block of K and V as stored in the cache (16-bit words).
 template <int D>
 struct GqaWaveLds {
-  _Float16 k[kBlock][D + kKPad];    // K of one block, row r holds token swap23(r)
-  _Float16 vt[D][kBlock + kVtPad];  // V of one block, transposed
+  uint16_t k[kBlock][D + kKPad];       // K, row r holds token swap23(r)
+  uint16_t v[kBlock][D + v_pad<D>()];  // V, token-major
 };
 
-// Adds x to a range-check sum; the empty asm pins the check next to the
-// conversion it checks (left free, the compiler sinks it into the next block
-// and keeps the converted words alive until then).
-__device__ inline void fold_check(float& chk, float x) {
-  chk += x;
-  asm volatile("" : "+v"(chk));
+// The cache's element type and its 32x32x16 product.  kPBias: the
+// probabilities go to the P.V product as 2^kPBias p (fp16: p <= 2^8 under the
+// lazy rescale, so 2^15 at most); kScaleQ: each slot's query is brought to
+// [2^14, 2^15) by a power of two before it is split.
+template <typename T>
+struct Split32;
+
+template <>
+struct Split32<Bf16> {
+  typedef __bf16 E;
+  typedef __bf16 E8 __attribute__((ext_vector_type(8)));
+  static constexpr float kPBias = 0.0f;
+  static constexpr bool kScaleQ = false;
+  __device__ static float16x mm(E8 x, E8 y, float16x c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(x, y, c, 0, 0, 0);
+  }
+};
+
+template <>
+struct Split32<_Float16> {
+  typedef _Float16 E;
+  typedef half8 E8;
+  static constexpr float kPBias = 7.0f;
+  static constexpr bool kScaleQ = true;
+  __device__ static float16x mm(E8 x, E8 y, float16x c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(x, y, c, 0, 0, 0);
+  }
+};
+
+// V^T fragment (A operand of the 32x32x16 product) for dims 32 d .. 32 d + 31
+// and tokens k0 + 8 hh .. k0 + 8 hh + 7: lane (j, hh) gets V[k0 + 8 hh + e][32 d + j],
+// e = 0..7.  ds_read_b64_tr_b16 transposes inside each group of 16 lanes:
+// lane i supplies 8 bytes of row i / 4 of a 4 x 16 block and receives column
+// i (lane layout checked on gfx950); two reads give the eight tokens.
+template <typename E8, int D>
+__device__ inline E8 vt_fragment(const GqaWaveLds<D>& w, int d, int k0, int j, int hh) {
+  typedef short short4x __attribute__((ext_vector_type(4)));
+  typedef short short8x __attribute__((ext_vector_type(8)));
+  typedef __attribute__((address_space(3))) short4x lds_short4x;
+  const int i = j & 15;
+  // C-style casts keep the LDS address arithmetic visible, so the constant
+  // part of the address goes into the instructions' offset field
+  const lds_short4x* lo_p =
+      (const lds_short4x*)(&w.v[k0 + 8 * hh + (i >> 2)][32 * d + (j & 16) + 4 * (i & 3)]);
+  const lds_short4x* hi_p =
+      (const lds_short4x*)(&w.v[k0 + 8 * hh + 4 + (i >> 2)][32 * d + (j & 16) + 4 * (i & 3)]);
+  const short4x lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(const_cast<lds_short4x*>(lo_p));
+  const short4x hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(const_cast<lds_short4x*>(hi_p));
+  const short8x x = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+  return __builtin_bit_cast(E8, x);
 }
 
 // One wave's partition pass: up to 32 query slots that read the same KV
 // head and the same pages, keys [lo, hi) of block table row `bt`.  Lane
-// (j, hh) serves slot j: its query starts at element q_off of a.q, and its
-// result goes either normalised to a.out at element out_off (`direct`, the
-// row's only partition) or as the partition state pi of a.part_acc /
-// a.part_ml.  Slots j >= gc are padding (zero query, nothing written).
-// Returns true (wave-uniform) when an fp16 operand of the pass was inf or
-// NaN: a scaled query of magnitude >= 65520 or, for a bf16 cache, a K/V value
-// >= 65536.  The state is then unusable and the caller recomputes the unit
-// in fp32.
+// (j, hh) serves slot j: its query starts at element q_off of a.q.  Slots
+// j >= gc are padding (zero query, nothing written by the caller).  Returns
+// the state in o / m / l in the ordinary units (m minus kPBias: o and l
+// carry the 2^kPBias factor of the probabilities); l is this lane's share of
+// the sum.
 template <typename T, int D>
-__device__ inline bool gqa_wave_run(const RowAttnArgs& a, GqaWaveLds<D>& w, int lane, int kvh,
+__device__ inline void gqa_wave_run(const RowAttnArgs& a, GqaWaveLds<D>& w, int lane, int kvh,
                                     int gc, const int32_t* bt, int lo, int hi, int64_t q_off,
                                     float16x (&o)[D / 32], float& m, float& l) {
-  constexpr bool kCheckKv = std::is_same_v<T, Bf16>;
+  using Ops = Split32<T>;
+  using E = typename Ops::E;
+  using E8 = typename Ops::E8;
   constexpr int kDC16 = D / 16;     // QK k-steps
   constexpr int kDB = D / 32;       // 32-dim output blocks
   constexpr int kDC = D / 8;        // 16-byte chunks per head row
   constexpr int kTpi = 64 / kDC;    // tokens per wave-wide load (kDC lanes per row)
   constexpr int kLi = kBlock / kTpi;   // loads per block, for K and for V
-  constexpr int kG = kLi / 2;       // consecutive V tokens per lane and page
-  static_assert(kTpi <= 16 && kG >= 1, "head_dim");
+  static_assert(kTpi <= 16 && kLi >= 2, "head_dim");
   const int j = lane & 31;
   const int hh = lane >> 5;
 
@@ -96,33 +154,63 @@ __device__ inline bool gqa_wave_run(const RowAttnArgs& a, GqaWaveLds<D>& w, int 
   const int page0 = lo >> 4;
   const int idv = bt[min(page0 + lane, a.MB - 1)];
 
-  // Q^T fragments: lane (j, hh) holds slot j, dims 16c + 8hh .. +7.
-  half8 qf[kDC16];
-  float chk = 0.0f;   // range check of the fp16 words this lane made
+  // Q^T fragments, split: lane (j, hh) holds slot j, dims 16c + 8hh .. +7.
+  // qexp: the power of two the query was multiplied by (kScaleQ), taken back
+  // out of every score.
+  E8 qh[kDC16], ql[kDC16];
+  int qexp = 0;
   {
     const float sc = j < gc ? a.qscale : 0.0f;
     const float* qp = a.q + q_off + 8 * hh;
+    float xq[kDC16][8];
+    float amax = 0.0f;
 #pragma unroll
     for (int c = 0; c < kDC16; ++c) {
       const float4 x0 = *reinterpret_cast<const float4*>(qp + 16 * c);
       const float4 x1 = *reinterpret_cast<const float4*>(qp + 16 * c + 4);
-      const uint4 qw = make_uint4(pack_f16(x0.x * sc, x0.y * sc), pack_f16(x0.z * sc, x0.w * sc),
-                                  pack_f16(x1.x * sc, x1.y * sc), pack_f16(x1.z * sc, x1.w * sc));
-      chk = f16_check(qw, chk);
-      qf[c] = __builtin_bit_cast(half8, qw);
+      const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        xq[c][e] = xs[e] * sc;
+        amax = fmaxf(amax, fabsf(xq[c][e]));
+      }
+    }
+    if constexpr (Ops::kScaleQ) {
+      // the slot's largest |element| (its dims are split over lanes j and
+      // j + 32); 2^qexp * amax lands in [2^14, 2^15), and a zero or
+      // non-finite query keeps qexp = 0
+      amax = max_halves(amax);
+      if (amax > 0.0f && __builtin_isfinite(amax)) qexp = 15 - __builtin_amdgcn_frexp_expf(amax);
+    }
+#pragma unroll
+    for (int c = 0; c < kDC16; ++c) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float x = Ops::kScaleQ ? ldexpf(xq[c][e], qexp) : xq[c][e];
+        const E h = (E)x;
+        qh[c][e] = h;
+        ql[c][e] = (E)(x - (float)h);
+      }
+    }
+    // Keep the split query in registers: without this anchor the compiler
+    // may re-load and re-split it on every block to save registers.
+#pragma unroll
+    for (int c = 0; c < kDC16; ++c) {
+      uint4& uh = reinterpret_cast<uint4&>(qh[c]);
+      uint4& ul = reinterpret_cast<uint4&>(ql[c]);
+      asm volatile("" : "+v"(uh.x), "+v"(uh.y), "+v"(uh.z), "+v"(uh.w));
+      asm volatile("" : "+v"(ul.x), "+v"(ul.y), "+v"(ul.z), "+v"(ul.w));
     }
   }
   const int64_t tok = (int64_t)a.Hkv * D;           // elements between tokens of a page
   // Loads are coalesced: kDC neighbouring lanes read one token's head row.
-  // Lane L holds chunk L % kDC of token slot L / kDC.  K load u covers
-  // tokens kTpi*u + slot; V load u of page half ph covers tokens
-  // 16*ph + kG*slot + u % kG, so that each lane ends up with kG consecutive
-  // tokens of the same 8 dims for its transposed LDS store.  Every load
-  // stays inside one 16-token page (wave-uniform block id).
+  // Lane L holds chunk L % kDC of token slot L / kDC; load u of K and of V
+  // covers tokens kTpi*u + slot, which stay inside one 16-token page
+  // (wave-uniform block id).
   const int ck = lane % kDC;
   const int slot = lane / kDC;
-  const T* kbase = reinterpret_cast<const T*>(a.k) + kvh * D + 8 * ck;
-  const T* vbase = reinterpret_cast<const T*>(a.v) + kvh * D + 8 * ck;
+  const uint16_t* kbase = reinterpret_cast<const uint16_t*>(a.k) + kvh * D + 8 * ck;
+  const uint16_t* vbase = reinterpret_cast<const uint16_t*>(a.v) + kvh * D + 8 * ck;
 
   uint4 kr[kLi], vr[kLi];
   // Loads of the block whose first page is relative page pg.
@@ -137,43 +225,17 @@ __device__ inline bool gqa_wave_run(const RowAttnArgs& a, GqaWaveLds<D>& w, int 
     }
 #pragma unroll
     for (int u = 0; u < kLi; ++u) {
-      const int ph = u / kG;
-      const int t = kG * slot + u % kG;                // token in the page
-      vr[u] = load16_stream(vbase + ((ph == 0 ? b0 : b1) + t) * tok);
+      const int t = kTpi * u + slot;
+      vr[u] = load16_stream(vbase + ((t < 16 ? b0 : b1) + (t & 15)) * tok);
     }
   };
-  // Registers -> LDS: K rows in swapped order, V transposed.
+  // Registers -> LDS as stored: K rows in swapped order, V rows in order.
   auto store_block = [&](GqaWaveLds<D>& w) {
 #pragma unroll
     for (int u = 0; u < kLi; ++u) {
       const int t = kTpi * u + slot;
-      const uint4 h = to_f16x8<T>(kr[u]);
-      if constexpr (kCheckKv) fold_check(chk, f16_check(h, 0.0f));
-      *reinterpret_cast<uint4*>(&w.k[swap_bits23(t)][8 * ck]) = h;
-    }
-#pragma unroll
-    for (int ph = 0; ph < 2; ++ph) {
-      const uint4* x = vr + kG * ph;
-      uint4 h1;   // kG == 1: the lane's 8 dims of one token, converted at once
-      if constexpr (kG == 1) {
-        h1 = to_f16x8<T>(x[0]);
-        if constexpr (kCheckKv) fold_check(chk, f16_check(h1, 0.0f));
-      }
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        _Float16* dst = &w.vt[8 * ck + e][16 * ph + kG * slot];
-        if constexpr (kG == 4) {
-          const uint32_t w0 = pack_col<T>(x[0], x[1], e), w1 = pack_col<T>(x[2], x[3], e);
-          if constexpr (kCheckKv) fold_check(chk, f16_check(w0, w1, 0.0f));
-          *reinterpret_cast<uint2*>(dst) = make_uint2(w0, w1);
-        } else if constexpr (kG == 2) {
-          const uint32_t w0 = pack_col<T>(x[0], x[1], e);
-          if constexpr (kCheckKv) fold_check(chk, f16_check(w0, w0, 0.0f));
-          *reinterpret_cast<uint32_t*>(dst) = w0;
-        } else {
-          *dst = __builtin_bit_cast(half8, h1)[e];
-        }
-      }
+      *reinterpret_cast<uint4*>(&w.k[swap_bits23(t)][8 * ck]) = kr[u];
+      *reinterpret_cast<uint4*>(&w.v[t][8 * ck]) = vr[u];
     }
   };
 
@@ -181,7 +243,7 @@ __device__ inline bool gqa_wave_run(const RowAttnArgs& a, GqaWaveLds<D>& w, int 
   for (int d = 0; d < kDB; ++d)
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[d][r] = 0.0f;
-  m = kNegBig;   // running max of head j (shared by lanes j, j + 32)
+  m = kNegBig;   // running max of slot j (shared by lanes j, j + 32)
   l = 0.0f;      // this lane's share of the running sum
 
   load_block(0);
@@ -192,13 +254,20 @@ __device__ inline bool gqa_wave_run(const RowAttnArgs& a, GqaWaveLds<D>& w, int 
     store_block(w);
     load_block(((t0 - lo) >> 4) + 2);
 
-    half8 kf[kDC16];
+    E8 kf[kDC16];
 #pragma unroll
-    for (int c = 0; c < kDC16; ++c)
-      kf[c] = *reinterpret_cast<const half8*>(&w.k[j][16 * c + 8 * hh]);
-    float16x s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[0], qf[0], (float16x)0.0f, 0, 0, 0);
+    for (int c = 0; c < kDC16; ++c) kf[c] = *reinterpret_cast<const E8*>(&w.k[j][16 * c + 8 * hh]);
+    float16x s = Ops::mm(kf[0], qh[0], (float16x)0.0f);
+    s = Ops::mm(kf[0], ql[0], s);
 #pragma unroll
-    for (int c = 1; c < kDC16; ++c) s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[c], qf[c], s, 0, 0, 0);
+    for (int c = 1; c < kDC16; ++c) {
+      s = Ops::mm(kf[c], qh[c], s);
+      s = Ops::mm(kf[c], ql[c], s);
+    }
+    if constexpr (Ops::kScaleQ) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[r] = ldexpf(s[r], -qexp);
+    }
     // register r of half hh holds token t0 + 16 * (r / 8) + 8 * hh + r % 8
     if (t0 + kBlock > hi) {
 #pragma unroll
@@ -222,28 +291,26 @@ __device__ inline bool gqa_wave_run(const RowAttnArgs& a, GqaWaveLds<D>& w, int 
         for (int r = 0; r < 16; ++r) o[d][r] *= corr;
       m = m_new;
     }
-    half8 pk[2];
+    E8 ph[2], pl[2];
+    const float mb = m - Ops::kPBias;
 #pragma unroll
-    for (int hf = 0; hf < 2; ++hf) {
-      uint32_t w[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        w[i] = pack_f16(fast_exp2(s[8 * hf + 2 * i] - m), fast_exp2(s[8 * hf + 2 * i + 1] - m));
-        l = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2x, w[i]),
-                                   (half2x){(_Float16)1.0f, (_Float16)1.0f}, l, false);
-      }
-      pk[hf] = __builtin_bit_cast(half8, make_uint4(w[0], w[1], w[2], w[3]));
+    for (int r = 0; r < 16; ++r) {
+      const float p = fast_exp2(s[r] - mb);       // masked tokens: exp2(-inf) = 0
+      l += p;
+      const E h = (E)p;
+      ph[r >> 3][r & 7] = h;
+      pl[r >> 3][r & 7] = (E)(p - (float)h);
     }
 #pragma unroll
     for (int kc = 0; kc < 2; ++kc)
 #pragma unroll
       for (int d = 0; d < kDB; ++d) {
-        const half8 vf =
-            *reinterpret_cast<const half8*>(&w.vt[d * 32 + j][kc * 16 + 8 * hh]);
-        o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pk[kc], o[d], 0, 0, 0);
+        const E8 vf = vt_fragment<E8, D>(w, d, 16 * kc, j, hh);
+        o[d] = Ops::mm(vf, ph[kc], o[d]);
+        o[d] = Ops::mm(vf, pl[kc], o[d]);
       }
   }
-  return __builtin_amdgcn_ballot_w64(f16_check_failed(chk)) != 0;
+  m -= Ops::kPBias;
 }
 
 // Result of slot j of a wave: lane (j, hh) owns dims d*32 + 8g + 4hh + 0..3.
@@ -455,10 +522,6 @@ void shared_pages_kernel(RowAttnArgs a, SharePlanArgs s) {
   constexpr int kState = 16 * kDB + 2;           // floats per lane: o, m, l
   static_assert(kState * 64 * sizeof(float) <= sizeof(GqaWaveLds<D>), "state exchange");
   __shared__ GqaWaveLds<D> lds[kGqaWaves];
-  // per wave: its pass hit an fp16 operand it cannot hold (two sets, by item
-  // parity, so that a wave's flag for the next item never overwrites one
-  // another wave may still be reading)
-  __shared__ int range_fail[2][kGqaWaves];
   const int lane = threadIdx.x & 63;
   const int wv = threadIdx.x >> 6;
   const int j = lane & 31;
@@ -492,34 +555,17 @@ void shared_pages_kernel(RowAttnArgs a, SharePlanArgs s) {
     t.row_h = (int64_t)t.mb * a.H + t.kvh * G + js % G;
     return t;
   };
-  int parity = 0;
-  for (int item = blockIdx.x; item < total * a.Hkv; item += gridDim.x, parity ^= 1) {   // workgroup-uniform
+  for (int item = blockIdx.x; item < total * a.Hkv; item += gridDim.x) {   // workgroup-uniform
     float16x o[kDB];
     float m, l;
     {
       const Slot t = slot_of(item);
       const int lo = t.p * a.part_tokens + wv * span;
       const int hi = wv == kGqaWaves - 1 ? (t.p + 1) * a.part_tokens : lo + span;
-      const bool fail = gqa_wave_run<T, D>(a, lds[wv], lane, t.kvh, t.gc,
-                                           a.bt + (int64_t)t.un.z * a.MB, lo, hi, t.row_h * D, o,
-                                           m, l);
-      if (lane == 0) range_fail[parity][wv] = fail;
+      gqa_wave_run<T, D>(a, lds[wv], lane, t.kvh, t.gc, a.bt + (int64_t)t.un.z * a.MB, lo, hi,
+                         t.row_h * D, o, m, l);
     }
     __syncthreads();   // every wave is done with its K/V tiles
-    bool fail = false;
-#pragma unroll
-    for (int w = 0; w < kGqaWaves; ++w) fail |= range_fail[parity][w] != 0;
-    if (fail) {
-      // An operand fp16 cannot hold: hand the group's (sequence, partition)
-      // pairs back to the partition kernel, which runs after this one and
-      // computes them like any other partition.
-      if (wv == 0) {
-        const Slot t = slot_of(item);
-        if (j < t.un.y && lane < 32)
-          s.skip[(int64_t)s.members[(int64_t)t.p * a.B + t.un.x + j] * a.P + t.p] = 0;
-      }
-      continue;
-    }
     float* xs = reinterpret_cast<float*>(&lds[wv]);
     if (wv > 0) {
 #pragma unroll

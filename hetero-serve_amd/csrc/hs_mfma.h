@@ -1,6 +1,6 @@
-// Helpers shared by the matrix-core kernels (hs_prefill_mfma.hip,
-// hs_decode_gqa.hip): fp16 operand packing and the lane-half reductions of a
-// 32x32 MFMA accumulator.
+// Helpers shared by the 32x32 matrix-core kernels (hs_prefill_mfma.hip,
+// hs_decode_gqa.hip): the prefill's fp16 operand packing and range check, and
+// the lane-half reductions of a 32x32 MFMA accumulator.
 #pragma once
 
 #include "hs_common.h"
@@ -70,20 +70,6 @@ __device__ inline uint4 to_f16x8(const uint4& w) {
 template <>
 __device__ inline uint4 to_f16x8<_Float16>(const uint4& w) {
   return w;
-}
-
-// Element e of two chunks, as the fp16 pair (x[e], y[e]).
-template <typename T>
-__device__ inline uint32_t pack_col(const uint4& x, const uint4& y, int e) {
-  return pack_f16(elem_f32<T>(x, e), elem_f32<T>(y, e));
-}
-
-template <>
-__device__ inline uint32_t pack_col<_Float16>(const uint4& x, const uint4& y, int e) {
-  const uint32_t xw = e < 2 ? x.x : e < 4 ? x.y : e < 6 ? x.z : x.w;
-  const uint32_t yw = e < 2 ? y.x : e < 4 ? y.y : e < 6 ? y.z : y.w;
-  // v_perm_b32: bytes {x half, y half} of the selected 16-bit lanes
-  return __builtin_amdgcn_perm(yw, xw, (e & 1) ? 0x07060302u : 0x05040100u);
 }
 
 // Both lane halves' values of x: {lanes 0-31, lanes 32-63} seen from each lane.

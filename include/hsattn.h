@@ -159,9 +159,9 @@ int hs_decode_noalloc(const float* q, const void* k_cache, const void* v_cache, 
  * hs_decode(num_splits = 0, partition_tokens) computes.  A partition of
  * partition_tokens keys that is full in at least 4 sequences with identical
  * block ids is read once for up to 32 (sequence, head) query slots of a KV
- * head on the matrix cores (fp16 operands, fp32 accumulation: within 1e-3 of
- * the fp32 path); every other
- * partition runs as in hs_decode.  The grouping is found on the device by
+ * head on the matrix cores (K/V as stored, q and the probabilities split
+ * into two 16-bit terms each, fp32 accumulation: fp32-grade results); every
+ * other partition runs as in hs_decode.  The grouping is found on the device by
  * one small kernel per call.  Serves fp16/bf16 KV with BS == 16, D in
  * {32, 64, 128}, partitions of at most 1024 tokens, at most 16 query heads per
  * KV head and B <= 2048; other calls run hs_decode's path unchanged.

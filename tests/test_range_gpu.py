@@ -1,16 +1,15 @@
 """Operands beyond fp16 range on the matrix-core paths.
 
-The MFMA prefill and the shared-page decode feed fp16 operands to the matrix
-cores.  A bf16 cache can hold values
-fp16 cannot (|x| >= 65536 rounds to inf), and a large query overflows fp16
-once scaled.  The reference never meets this: its WMMA path admits fp16
-caches only (paged_attn_wmma.py:266-267, :372-387) and its torch oracle
-computes in fp32 (paged_attn.py:255-298, paged_attn_prefill.py:281-322).
-Here each such kernel checks the operands it converts and recomputes an
-affected unit in fp32 (the shared-page decode hands it back to the partition
-kernel), so the result must match the fp32 oracle.  The grouped-query decode
-(split operands of the cache's own type, the query scaled into range)
-converts nothing and needs no fallback; its tests here check exactly that.
+The MFMA prefill feeds fp16 operands to the matrix cores.  A bf16 cache can
+hold values fp16 cannot (|x| >= 65536 rounds to inf), and a large query
+overflows fp16 once scaled.  The reference never meets this: its WMMA path
+admits fp16 caches only (paged_attn_wmma.py:266-267, :372-387) and its torch
+oracle computes in fp32 (paged_attn.py:255-298, paged_attn_prefill.py:281-322).
+Here the prefill checks the operands it converts and recomputes an affected
+unit in fp32, so the result must match the fp32 oracle.  The grouped-query
+and shared-page decodes (split operands of the cache's own type, the query
+scaled into range for fp16 caches) convert nothing and need no fallback;
+their tests here check exactly that.
 
 Tolerance, per element: 2e-3 * max(1, |oracle|) -- the north-star 2e-3
 max-abs where outputs are O(1), 2e-3 relative where a planted V value makes
@@ -285,9 +284,10 @@ def test_split_decode_query_and_cache_range(H, Hkv, D, dtype):
 
 @pytest.mark.parametrize("H,Hkv,D", [(8, 8, 128), (32, 4, 128), (16, 4, 64)])
 def test_shared_pages_operands_beyond_fp16(H, Hkv, D):
-    """A shared prefix page holding 1e30 sends the group back to the partition
-    kernel; every sequence against the fp32 oracle.  A large value in a
-    private page goes through the partition kernel's own path."""
+    """A shared prefix page holding 1e30 goes through the shared-page kernel's
+    split-operand products as stored (bf16 operands, fp32 accumulation);
+    every sequence against the fp32 oracle.  A large value in a private page
+    goes through the partition kernel's own path."""
     from heteroserve import _hip
 
     rng = np.random.default_rng(H + Hkv + D)
