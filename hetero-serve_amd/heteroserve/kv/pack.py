@@ -209,6 +209,7 @@ def block_table_tensor(tables, pad_to=None, device="cuda"):
     int32 ``[len(tables), width]`` table, -1 padded, ``width = pad_to`` or the
     longest table (1 when there are no tables); longer tables are truncated.
     One host-to-device copy of all ids instead of one per sequence."""
+    import array
     import itertools
 
     import numpy as np
@@ -221,10 +222,19 @@ def block_table_tensor(tables, pad_to=None, device="cuda"):
     out = torch.empty((B, width), dtype=torch.int32, device=device)
     if B == 0 or width == 0:
         return out
-    # one conversion of all ids (the Python-int conversion is the host cost)
+    # one conversion of all ids (the Python-int conversion is the host cost:
+    # array.fromlist converts a list of ints ~3x faster than numpy does)
     lens = [min(len(t), width) for t in tables]
-    flat = np.array(list(itertools.chain.from_iterable(
-        t if len(t) <= width else list(t)[:width] for t in tables)), dtype=np.int64)
+    ids = array.array("l" if array.array("l").itemsize == 8 else "q")
+    try:
+        for t in tables:
+            ids.fromlist(t if type(t) is list and len(t) <= width else list(t)[:width])
+        flat = np.frombuffer(ids, dtype=np.int64)
+    except TypeError:   # ids that are not integers: numpy's conversion
+        flat = np.array(list(itertools.chain.from_iterable(list(t)[:width] for t in tables)),
+                        dtype=np.int64)
+    except OverflowError:
+        raise RuntimeError("value cannot be converted to type int32 without overflow") from None
     if flat.size and (flat.min() < -2 ** 31 or flat.max() >= 2 ** 31):
         raise RuntimeError("value cannot be converted to type int32 without overflow")
     off = np.zeros(B + 1, dtype=np.int64)
