@@ -28,31 +28,50 @@ up by inheritance:
 
 from __future__ import annotations
 
-from typing import Sequence
-
 from .. import _hip
 
 
-def _normalise_ids(block_ids, num_blocks: int) -> list[int]:
-    """Block ids as Python ints, negatives wrapped as torch indexing does."""
+def _normalise_ids(block_ids, num_blocks: int):
+    """Block ids as an int64 numpy array, negatives wrapped as torch indexing
+    does; the first id outside [-num_blocks, num_blocks) raises IndexError.
+    Integer lists, arrays and tensors are converted in one numpy pass; other
+    elements (floats, objects, values beyond int64) go through int() one by
+    one, as torch's indexing would take them."""
+    import numpy as np
     import torch
 
-    if torch.is_tensor(block_ids):
-        block_ids = block_ids.detach().to("cpu").reshape(-1).tolist()
-    out = []
-    for raw in block_ids:
-        i = int(raw)
-        if not -num_blocks <= i < num_blocks:
-            raise IndexError(
-                f"index {i} is out of bounds for dimension 2 with size {num_blocks}")
-        out.append(i + num_blocks if i < 0 else i)
-    return out
+    ids = None
+    try:
+        if torch.is_tensor(block_ids):
+            if not block_ids.is_floating_point() and not block_ids.is_complex():
+                ids = block_ids.detach().to("cpu").reshape(-1).to(torch.int64).numpy()
+        else:
+            arr = np.asarray(block_ids).reshape(-1)
+            if arr.dtype.kind in "ib" or (arr.dtype.kind == "u" and arr.dtype.itemsize < 8):
+                ids = arr.astype(np.int64, copy=False)
+    except (TypeError, ValueError, OverflowError):
+        ids = None
+    if ids is None:   # element by element
+        if torch.is_tensor(block_ids):
+            block_ids = block_ids.detach().to("cpu").reshape(-1).tolist()
+        vals = [int(raw) for raw in block_ids]
+        for i in vals:
+            if not -num_blocks <= i < num_blocks:
+                raise IndexError(
+                    f"index {i} is out of bounds for dimension 2 with size {num_blocks}")
+        ids = np.array(vals, dtype=np.int64)
+    bad = (ids < -num_blocks) | (ids >= num_blocks)
+    if bad.any():
+        i = int(ids[int(np.argmax(bad))])
+        raise IndexError(f"index {i} is out of bounds for dimension 2 with size {num_blocks}")
+    return np.where(ids < 0, ids + num_blocks, ids)
 
 
-def _ids_tensor(ids: Sequence[int], device):
+def _ids_tensor(ids, device):
+    import numpy as np
     import torch
 
-    return torch.as_tensor(ids, dtype=torch.int64).to(device, non_blocking=False)
+    return torch.from_numpy(np.ascontiguousarray(ids, dtype=np.int64)).to(device)
 
 
 def _check_pool(pool) -> None:
@@ -73,7 +92,7 @@ def export_blocks_device(pool, block_ids):
     ids = _normalise_ids(block_ids, pool.shape[2])
     L, _, _, BS, H, D = pool.shape
     out = torch.empty((len(ids), L, 2, BS, H, D), dtype=pool.dtype, device=pool.device)
-    if ids:
+    if len(ids):
         _hip.kv_pack(pool, _ids_tensor(ids, pool.device), out)
     return out
 
@@ -86,10 +105,13 @@ def write_blocks_device(pool, block_ids, payload) -> None:
     last payload entry for it wins, which is what the reference's sequential
     loop leaves behind.
     """
+    import numpy as np
+    import torch
+
     _hip.lib("KV unpack HIP kernel")
     _check_pool(pool)
     ids = _normalise_ids(block_ids, pool.shape[2])
-    if not ids:
+    if not len(ids):
         return
     data = payload.to(device=pool.device, dtype=pool.dtype)
     block_shape = tuple(pool.shape[:2]) + tuple(pool.shape[3:])
@@ -97,11 +119,12 @@ def write_blocks_device(pool, block_ids, payload) -> None:
         raise RuntimeError(
             f"payload must be [n >= {len(ids)}, {', '.join(map(str, block_shape))}], "
             f"got {list(data.shape)}")
-    last = {blk: i for i, blk in enumerate(ids)}
-    if len(last) != len(ids):  # duplicates: keep each block's final write
-        order = sorted(last.items(), key=lambda kv: kv[1])
-        ids = [blk for blk, _ in order]
-        data = data[[i for _, i in order]]
+    n = len(ids)
+    uniq, first_rev = np.unique(ids[::-1], return_index=True)
+    if len(uniq) != n:  # duplicates: keep each block's final write, in write order
+        last = np.sort(n - 1 - first_rev)
+        ids = ids[last]
+        data = data[torch.from_numpy(last).to(data.device)]
     data = data[: len(ids)].contiguous()
     _hip.kv_unpack(pool, _ids_tensor(ids, pool.device), data)
 
@@ -112,6 +135,7 @@ def gather_kv_batch(pool, tables, length: int, layer: int):
     tables is a list of per-sequence block-id lists, as the reference takes;
     every list must cover `length` tokens.
     """
+    import numpy as np
     import torch
 
     _hip.lib("KV gather HIP kernel")
@@ -132,7 +156,7 @@ def gather_kv_batch(pool, tables, length: int, layer: int):
     v_out = torch.empty_like(k_out)
     if B == 0 or length == 0:
         return k_out, v_out
-    bt = torch.as_tensor(rows, dtype=torch.int32).reshape(B, need).to(pool.device)
+    bt = torch.from_numpy(np.stack(rows).astype(np.int32)).reshape(B, need).to(pool.device)
     _hip.kv_gather(pool[layer, 0], bt, length, k_out)
     _hip.kv_gather(pool[layer, 1], bt, length, v_out)
     return k_out, v_out
