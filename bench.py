@@ -943,7 +943,10 @@ def main() -> int:
         "data": "synthetic (seeded N(0,1) KV and queries, seeded block tables)",
         "config": config,
         "roofline": roofline(
-            "hbm", "row_attn_part_kernel", dec["bytes"], dec["kernel_ms"],
+            "hbm",
+            LEG_KERNELS[args.config][0].replace("hs::", "") if args.config in LEG_KERNELS
+            else "row_attn_part_kernel",
+            dec["bytes"], dec["kernel_ms"],
             leg_traffic(args.config)
             if args.config in LEG_KERNELS and args.config != "C2-gqa" and not args.partition
             else None),

@@ -97,11 +97,11 @@ struct DecodePlan {
 //
 // bf16 and fp16 caches with 2 or more query heads per KV head run the
 // split-operand matrix-core decode, whose workgroups of splitmm_waves(G)
-// waves share a partition: its own default (splitmm_default_partition, 512 or
-// 256 tokens) applies there.
+// waves share a partition: its own default (splitmm_default_partition: 768,
+// 384 or 256 tokens) applies there.
 //
 // Small grids: the partition is halved (down to 32 tokens, or one page per
-// wave) while the launch, estimated from the table's width, has fewer than 4
+// wave, and never below that floor) while the launch, estimated from the table's width, has fewer than 4
 // waves per CU.  Each wave then walks a few iterations instead of a long
 // serial chain.  Measured on C1 (8 sequences, 12 heads, contexts up to 512):
 // 20.1 us per step at 512 tokens, 14.8 at 64, 14.3 at 32, 15.8 at 16 (the
@@ -112,7 +112,7 @@ static int shrink_for_small_grid(int pt, int min_pt, int64_t waves_per_part, int
   if (cus <= 0) return pt;
   const int64_t max_ctx = (int64_t)MB * BS;
   while (pt > min_pt && sat_mul(waves_per_part, ceil_div(max_ctx, pt)) < 4 * (int64_t)cus)
-    pt /= 2;
+    pt = std::max(min_pt, pt / 2);
   return pt;
 }
 

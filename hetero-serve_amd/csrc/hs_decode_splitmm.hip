@@ -503,20 +503,31 @@ bool splitmm_applies(const RowAttnArgs& a, int kv_dtype, int D) {
          a.part_tokens <= kPage * kMaxPages;
 }
 
-// Waves per partition and the default partition: each wave walks about 128
-// tokens, and groups of at most 4 query heads (the least arithmetic per
-// byte) share a 512-token partition between 4 waves, so a quarter of the
-// partition states reach HBM.  Measured on C2's batch and contexts, 32 query
-// heads, bf16 (step, us, waves x partition tokens):
+// Waves per partition and the default partition.  Groups of at most 4 query
+// heads (the least arithmetic per byte) share a partition between 4 waves,
+// larger groups between 2, so a quarter (half) of the partition states reach
+// HBM.  Measured on C2's batch and contexts, 32 query heads, bf16 (step, us,
+// waves x partition tokens):
 //   G = 2:  226 (1 x 256)  217 (2 x 512)  213 (4 x 512)
 //   G = 4:  129 (1 x 256)  126 (2 x 512)  123 (4 x 512)
 //   G = 8:   80 (1 x 256)   77 (2 x 256)   78 (4 x 256)
 //   G = 16:  52 (1 x 128)   50 (2 x 256)   53 (4 x 256)
 //   G = 32:  51 (1 x 128)   49 (2 x 256)   53 (4 x 256)
-// At head dim 32 (1-KB head pages) 256 tokens measured best or within 4% for
-// every G (C2 contexts, fp16, 32 query heads: G = 2 / 4 / 8: 119 / 65 / 40 us).
+// The partition length is best at about 12 pages per wave (step, us, same
+// batch, partition tokens 256 / 384 / 512 / 640 / 768 / 896 / 1024):
+//   G = 2, D 128:  226 216 215 211 208 216 215
+//   G = 4, D 128:  126 119 122 117 117 121 138
+//   G = 8, D 128:   78  69  83  78  81  83 110
+//   G = 4, D 64:    72  69  75  69  68  73  89
+//   G = 2, D 64:   124 127 129 123 125 134 136
+// so 768 tokens for 4 waves and 384 for 2 (G = 8); G > 8 keeps 256.  At head
+// dim 32 (1-KB head pages) 256 tokens measured best or within 4% for every G
+// (C2 contexts, fp16, 32 query heads: G = 2 / 4 / 8: 119 / 65 / 40 us).
 int splitmm_waves(int G) { return G <= 4 ? 4 : 2; }
-int splitmm_default_partition(int G, int D) { return D == 32 || G > 4 ? 256 : 512; }
+int splitmm_default_partition(int G, int D) {
+  if (D == 32 || G > 8) return 256;
+  return G <= 4 ? 768 : 384;
+}
 
 int64_t splitmm_grid(const RowAttnArgs& a) {
   const int G = a.H / a.Hkv;

@@ -120,8 +120,9 @@ size_t hs_decode_workspace_bytes(int B, int H, int Hkv, int D, int BS, int MB, i
  *   partition_tokens  used when num_splits == 0; 0 = library default (512
  *                tokens, fewer for GQA groups and for grids of fewer than 4
  *                waves per CU; fp16 and bf16 caches with 2 or more query
- *                heads per KV head: 512 tokens up to 4 heads per KV head at
- *                head dim 64 and 128, 256 otherwise).
+ *                heads per KV head, head dim 64 and 128: 768 tokens up to 4
+ *                heads per KV head, 384 up to 8, 256 otherwise and at head
+ *                dim 32).
  *                Must be a multiple of 16.
  *   workspace    device scratch of hs_decode_workspace_bytes(...) bytes
  *                (may be NULL when that is 0).

@@ -148,8 +148,8 @@ def test_workspace_size_formula(lib):
     G query heads of a GQA group (G = 1, 2, 4, 8, the largest dividing H / Hkv),
     and 512 again when H / Hkv >= 8 and Hkv * ceil(H / Hkv / 32) <= 2.  bf16
     caches with 2 or more query heads per KV head (16-token pages, head_dim
-    64/128) default to 512 tokens up to 4 heads per KV head and 256 above;
-    the query takes no dtype, so it sizes for the shorter of the two."""
+    64/128) default to 768 tokens up to 4 heads per KV head, 384 up to 8 and
+    256 above; the query takes no dtype, so it sizes for the shortest."""
     B, H, D, BS, MB = 3, 5, 128, 16, 100
 
     def ws(P):
