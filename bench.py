@@ -26,7 +26,8 @@ The JSON line also carries:
                 peak for prefill)
   cpu_baseline  the CPU oracle (oracle/) on this host's cores, on the same
                 inputs, with the CPU model and thread count
-  secondary     C1 (small decode), C3 (long-context decode), C2 at Llama-3-8B's
+  secondary     C1 (small decode), C3 (long-context decode), batch 64 at a 4k
+                context (the decode target's shape), C2 at Llama-3-8B's
                 grouped-query geometry, C4 chunked prefill, the C5 migration
                 pack and unpack of 4096 blocks with a plain-copy ceiling, the
                 C5 KV write and the C5 mixed step
@@ -70,6 +71,7 @@ TRAFFIC_PROFILE = ROOT / "profiles" / "bench_legs_trace_and_traffic.md"
 LEG_KERNELS = {
     "C2": ("hs::row_attn_part_kernel<hs::Bf16, 128, true, 1>", 16384, "C2 alone"),
     "C3": ("hs::row_attn_part_kernel<hs::Bf16, 128, true, 1>", 32640, "every leg"),
+    "B64-4k": ("hs::row_attn_part_kernel<hs::Bf16, 128, true, 1>", 8192, "every leg"),
     "C1": ("hs::row_attn_part_kernel<_Float16, 64, true, 1>", None, "every leg"),
     "C2-gqa": ("hs::splitmm_part_kernel<hs::Bf16Ops, 128, true, 4>", None, "every leg"),
     "C4": ("hs::prefill_mfma_kernel<hs::Bf16, 128, 8>", 1536, "every leg"),
@@ -809,7 +811,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="C2", choices=["C1", "C2", "C2-gqa", "C3", "C5-decode"],
+    ap.add_argument("--config", default="C2", choices=["C1", "C2", "C2-gqa", "C3", "B64-4k", "C5-decode"],
                     help="decode configuration of the headline line")
     ap.add_argument("--partition", type=int, default=0,
                     help="decode partition tokens (0 = library default)")
@@ -861,6 +863,7 @@ def main() -> int:
     if not args.no_secondary:
         legs = [("C1", "row_attn_part_kernel<_Float16, 64, true, 1>", True, 0),
                 ("C3", "row_attn_part_kernel<Bf16, 128, true, 1>", False, 4),
+                ("B64-4k", "row_attn_part_kernel<Bf16, 128, true, 1>", False, 8),
                 ("C2-gqa", "splitmm_part_kernel<Bf16Ops, 128, true, 4>", False, 16)]
         for name, kernel, batched, n_seq in legs:
             if name == headline_name:

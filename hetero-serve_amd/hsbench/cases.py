@@ -8,6 +8,8 @@ The configurations are the reference path's headline workloads, restated:
       sigma 0.8) clipped to [64, 8192], 65536-block pool
   C2-gqa  C2's batch at Llama-3-8B's geometry: 32 query heads on 8 KV heads
   C3  long-context decode, B 16, 32 heads, D 128, bf16, ctx U[8192, 32768]
+  B64-4k  the north-star decode target's shape: C2's geometry with every one
+      of the 64 sequences at a 4096-token context
   C4  chunked causal prefill, 8 sequences with a cached prefix U[0, 4096] and a
       new chunk U[128, 2048], 32 heads, D 128, bf16
   C5  mixed step: a 1024-token chunk on a 2048-token prefix, 255 decode
@@ -234,6 +236,17 @@ def c3_decode(device, dtype=None) -> PagedCase:
                         rng=rng)
 
 
+def b64_4k_decode(device, dtype=None) -> PagedCase:
+    """Batch 64 at a 4k context (the decode target's "batch 64 / 4k
+    context"): C2's geometry, 32 heads MHA, D 128, bf16, every context 4096
+    tokens, pages scattered over a 65536-block pool."""
+    torch = _torch()
+    rng = np.random.default_rng(6)
+    ctx = np.full(64, 4096, dtype=np.int64)
+    return build_decode("B64-4k", ctx, 32, 32, 128, 65536, dtype or torch.bfloat16, device, 6,
+                        rng=rng)
+
+
 def c4_prefill(device, dtype=None) -> PagedCase:
     torch = _torch()
     rng = np.random.default_rng(3)
@@ -289,6 +302,7 @@ CONFIGS = {
     "C2": c2_decode,
     "C2-gqa": c2_gqa_decode,
     "C3": c3_decode,
+    "B64-4k": b64_4k_decode,
     "C4": c4_prefill,
     "C5-decode": c5_decode,
     "C5-prefill": c5_prefill,
