@@ -223,3 +223,40 @@ def test_disable_flag_is_honoured(monkeypatch):
     finally:
         monkeypatch.delenv("HETEROSERVE_DISABLE_CUDA_KERNEL")
         importlib.reload(_hip)
+
+
+def test_errors_are_per_thread(lib):
+    """hs_last_error is thread-local: hetero-serve's worker calls the library
+    from its executor thread (the step) and its event-loop thread (pack and
+    unpack) at the same time (worker.py:448, :527, :562-563), so one thread's
+    failure must never show up as the other's message.  Two threads fail in
+    different ways, many times over, and each reads back only its own."""
+    import threading
+
+    fake = ctypes.c_void_p(0x1000)
+    seen = {"a": set(), "b": set()}
+    start = threading.Barrier(2)
+
+    def fail_divisible():
+        start.wait()
+        for _ in range(2000):
+            rc = lib.hs_decode(fake, fake, fake, 0, 8, fake, fake, fake, 1, 6, 4, 64, 16, 2,
+                               0.1, 0, 0, None, 0, None)
+            assert rc == -1
+            seen["a"].add(lib.hs_last_error())
+
+    def fail_block_size():
+        start.wait()
+        for _ in range(2000):
+            rc = lib.hs_prefill(fake, fake, fake, 1, 8, fake, fake, fake, 1, 4, 4, 4, 64, 32, 2,
+                                0.1, 1, None, 0, None)
+            assert rc == -2
+            seen["b"].add(lib.hs_last_error())
+
+    threads = [threading.Thread(target=fail_divisible), threading.Thread(target=fail_block_size)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert len(seen["a"]) == 1 and b"divisible" in next(iter(seen["a"]))
+    assert len(seen["b"]) == 1 and b"block_size == 16" in next(iter(seen["b"]))
