@@ -263,6 +263,31 @@ def test_small_grid_default_partition():
     assert _maxerr(got, fixed) <= 1e-4
 
 
+@pytest.mark.parametrize("H,Hkv,D,dtype,lens", [
+    (32, 8, 128, torch.bfloat16, [1000, 3000]),          # G = 4: 768-token default
+    (32, 4, 128, torch.bfloat16, [700, 2100, 40]),       # G = 8: 384-token default
+    (12, 3, 64, torch.float16, [1500]),                  # G = 4 at head dim 64
+])
+def test_small_grid_gqa_default_partition(H, Hkv, D, dtype, lens):
+    """Grouped-query batches too small for the CUs: the split-operand
+    decode's default partition (768 tokens up to 4 query heads per KV head,
+    384 up to 8) is halved, never below one page per wave, until the grid
+    has 4 waves per CU; the lengths this visits (384, 192, 96, 64 and 48, 32
+    tokens) are no powers of two.  Results match the oracle and the one-pass
+    fp32 kernel to the split operands' precision, and a rerun is
+    bit-identical."""
+    from heteroserve import _hip
+
+    _, m2, _ = _mods()
+    pool, q, bt, ctx = _random_case(lens, H, Hkv, D, 16, dtype, seed=41)
+    kp, vp = pool[0, 0], pool[0, 1]
+    scale = D ** -0.5
+    got = _hip.decode(q, kp, vp, bt, ctx, scale, 0)
+    assert _maxerr(got, _oracle(q, kp, vp, bt, ctx, scale)) <= 5e-5
+    assert _maxerr(got, m2.paged_attention_v2(q, kp, vp, bt, ctx, scale)) <= 5e-5
+    assert torch.equal(got, _hip.decode(q, kp, vp, bt, ctx, scale, 0))
+
+
 @pytest.mark.parametrize("H,Hkv,D,dtype", [
     (32, 8, 128, torch.bfloat16),   # llama3-8b shape (config.py:85-93), G = 4
     (32, 1, 128, torch.bfloat16),   # MQA: two head chunks of 16
