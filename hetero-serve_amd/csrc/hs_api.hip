@@ -116,6 +116,14 @@ static int shrink_for_small_grid(int pt, int min_pt, int64_t waves_per_part, int
   return pt;
 }
 
+// The VALU kernel's partition before the small-grid cut.
+static int valu_partition(int H, int Hkv) {
+  const int G = H / Hkv;
+  return G >= 8 && (int64_t)Hkv * (((int64_t)G + 31) / 32) <= 2
+             ? kDefaultPartition
+             : std::min(kDefaultPartition, 1024 / row_attn_heads_per_wave(H, Hkv));
+}
+
 static int default_partition(int B, int H, int Hkv, int BS, int MB, int kv_dtype, int D) {
   const int G = H / Hkv;
   if (splitmm_serves(kv_dtype, BS, D, H, Hkv)) {
@@ -125,11 +133,24 @@ static int default_partition(int B, int H, int Hkv, int BS, int MB, int kv_dtype
                                  std::max(kMinDefaultPartition, BS * kw),
                                  sat_mul(B, Hkv, ceil_div(G, 16), kw), BS, MB);
   }
-  const int pt = G >= 8 && (int64_t)Hkv * (((int64_t)G + 31) / 32) <= 2
-                     ? kDefaultPartition
-                     : std::min(kDefaultPartition, 1024 / row_attn_heads_per_wave(H, Hkv));
-  return shrink_for_small_grid(pt, kMinDefaultPartition,
+  return shrink_for_small_grid(valu_partition(H, Hkv), kMinDefaultPartition,
                                sat_mul(B, Hkv, G / row_attn_heads_per_wave(H, Hkv)), BS, MB);
+}
+
+// Rows of at most this many keys (by the table's width) can take mode 3.
+constexpr int64_t kWgSplitMaxTokens = 1024;
+
+// The default decomposition of a small grid whose rows are short: instead of
+// partitions cut down to a few tokens and a merge launch, one workgroup per
+// (row, head group) splits the row's keys over its waves and combines their
+// states in LDS (mode 3; no workspace).  Applies where the VALU kernel runs
+// and the partition above was shortened for the grid.  Measured on C1 (8
+// sequences, 12 heads, head dim 64, fp16, up to 512 tokens): step 14.3 us
+// with 32-token partitions and the merge.
+static bool wg_split_applies(int B, int H, int Hkv, int BS, int MB, int kv_dtype, int D) {
+  if (splitmm_serves(kv_dtype, BS, D, H, Hkv)) return false;
+  if ((int64_t)MB * BS > kWgSplitMaxTokens) return false;
+  return default_partition(B, H, Hkv, BS, MB, kv_dtype, D) < valu_partition(H, Hkv);
 }
 
 // The workspace queries take no kv dtype: they size for the shortest default
@@ -301,7 +322,18 @@ static int decode_common(const float* q, const void* k_cache, const void* v_cach
   a.P = plan.P;
   a.qscale = scale * kLog2e;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (!shared_pages || !shared_pages_apply(a, kv_dtype, D)) return launch_row_attn(a, kv_dtype, D, st);
+  if (!shared_pages || !shared_pages_apply(a, kv_dtype, D)) {
+    // the default decomposition of a small grid of short rows: one
+    // workgroup per row and head group (the workspace, sized for the
+    // partitions above, goes unused)
+    if (num_splits == 0 && partition_tokens == 0 &&
+        wg_split_applies(B, H, Hkv, BS, MB, kv_dtype, D)) {
+      a.mode = 3;
+      a.part_tokens = 0;
+      a.P = 1;
+    }
+    return launch_row_attn(a, kv_dtype, D, st);
+  }
   SharePlanArgs sp{};
   sp.per_unit = share_per_unit(H, Hkv);
   sp.U = (int)share_unit_slots(B, sp.per_unit);   // B <= 2048 here (shared_pages_apply)

@@ -75,6 +75,75 @@ __attribute__((amdgpu_waves_per_eu(G >= 8 ? 2 : (D > 128 ? 3 : 4)))) void row_at
   }
 }
 
+// Small grids (mode 3): one workgroup per (row, head group of G) walks the
+// whole row, its W waves on W contiguous slices of the keys, and the waves'
+// states are combined through LDS, so a batch too small to fill the CUs gets
+// W times the waves without partition states or a merge launch.  Each wave
+// runs the same RowWalk as the partition kernel; the combine is the
+// log-sum-exp merge of paged_attn_v3.py:170-208 over the slices.
+template <typename T, int D, bool kPaged, int G, int W>
+__global__ __launch_bounds__(W * 64) void row_attn_wg_kernel(RowAttnArgs a) {
+  using Walk = RowWalk<T, D, kPaged, G>;
+  __shared__ float s_m[W][G], s_l[W][G];
+  __shared__ float s_acc[W][G][D];
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  const int n_hw = a.H / G;
+  const int row = (int)(blockIdx.x / n_hw);
+  const int h0 = (int)(blockIdx.x % n_hw) * G;
+  int b, end;
+  if (!row_geometry(a, row, b, end)) return;       // workgroup-uniform
+  const int64_t orow0 = ((int64_t)row * a.H + h0) * D;
+  if (end <= 0) {                                  // nothing to attend to: zero rows
+    for (int d = threadIdx.x; d < G * D; d += W * 64) a.out[orow0 + d] = 0.0f;
+    return;
+  }
+  // slices of whole load groups, so that no two waves load the same group
+  const int chunk = ((end + W - 1) / W + Walk::kTpl - 1) / Walk::kTpl * Walk::kTpl;
+  const int lo = wv * chunk;
+  const int hi = min(end, lo + chunk);
+  Walk w;
+  if (lo < hi) {
+    w.run(KvPages{a.k, a.v, a.Hkv, a.BS, a.NB}, a.q + orow0, a.qscale, h0 / (a.H / a.Hkv),
+          a.bt + (int64_t)b * a.MB, lo, hi);
+  } else {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      w.m[g] = kNegBig;
+      w.l[g] = 0.0f;
+#pragma unroll
+      for (int e = 0; e < Walk::kVec; ++e) w.acc[g][e] = 0.0f;
+    }
+  }
+  if (Walk::slot(lane) == 0) {
+    const int c = Walk::chunk(lane);
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+#pragma unroll
+      for (int e = 0; e < Walk::kVec; ++e) s_acc[wv][g][c * Walk::kVec + e] = w.acc[g][e];
+      if (c == 0) {
+        s_m[wv][g] = w.m[g];
+        s_l[wv][g] = w.l[g];
+      }
+    }
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < G * D; i += W * 64) {
+    const int g = i / D, d = i - g * D;
+    float mm = s_m[0][g];
+#pragma unroll
+    for (int v = 1; v < W; ++v) mm = fmaxf(mm, s_m[v][g]);
+    float l = 0.0f, o = 0.0f;
+#pragma unroll
+    for (int v = 0; v < W; ++v) {
+      const float wt = fast_exp2(s_m[v][g] - mm);   // an empty slice: exp2(-3e38 - mm) = 0
+      l = fmaf(s_l[v][g], wt, l);
+      o = fmaf(s_acc[v][g][d], wt, o);
+    }
+    a.out[orow0 + i] = l > 0.0f ? o / l : 0.0f;
+  }
+}
+
 // Log-sum-exp merge of the partition states of every (row, head) that has
 // more than one non-empty partition (reference: merge_splits_kernel,
 // paged_attn_v3.py:170-208).  One wave per (row, head), lanes over D.  The
@@ -181,14 +250,37 @@ static void launch_part(const RowAttnArgs& a, hipStream_t stream) {
     hipLaunchKernelGGL((row_attn_part_kernel<T, D, false, G>), grid, block, 0, stream, a);
 }
 
+// Waves of a mode-3 workgroup: 16 (4 per SIMD, at most 128 VGPRs each), or 8
+// where the walk holds more state (G = 8 heads, or head dim 256), as the
+// partition kernel's occupancy hints allow.  The waves' states take
+// W * G * D floats of LDS, 64 KiB at most.
+constexpr int wg_waves(int G, int D) { return G >= 8 || D > 128 ? 8 : 16; }
+
+template <typename T, int D, int G>
+static void launch_wg(const RowAttnArgs& a, hipStream_t stream) {
+  constexpr int W = wg_waves(G, D);
+  const int tpl = 64 / (D / Elem<T>::kVec);
+  const dim3 grid((unsigned)((int64_t)a.rows * (a.H / G))), block(W * 64);   // checked by the caller
+  if (a.BS % tpl == 0)
+    hipLaunchKernelGGL((row_attn_wg_kernel<T, D, true, G, W>), grid, block, 0, stream, a);
+  else
+    hipLaunchKernelGGL((row_attn_wg_kernel<T, D, false, G, W>), grid, block, 0, stream, a);
+}
+
+template <typename T, int D, int G>
+static void launch_mode(const RowAttnArgs& a, hipStream_t stream) {
+  if (a.mode == 3) launch_wg<T, D, G>(a, stream);
+  else launch_part<T, D, G>(a, stream);
+}
+
 template <typename T, int D>
 static void launch_typed(const RowAttnArgs& a, hipStream_t stream) {
   profile_begin(stream);
   switch (row_attn_heads_per_wave(a.H, a.Hkv)) {
-    case 8: launch_part<T, D, 8>(a, stream); break;
-    case 4: launch_part<T, D, 4>(a, stream); break;
-    case 2: launch_part<T, D, 2>(a, stream); break;
-    default: launch_part<T, D, 1>(a, stream); break;
+    case 8: launch_mode<T, D, 8>(a, stream); break;
+    case 4: launch_mode<T, D, 4>(a, stream); break;
+    case 2: launch_mode<T, D, 2>(a, stream); break;
+    default: launch_mode<T, D, 1>(a, stream); break;
   }
   profile_end(stream);
 }
@@ -221,7 +313,7 @@ int launch_row_attn(const RowAttnArgs& a, int kv_dtype, int D, hipStream_t strea
     gx = splitmm_grid(a);
   } else {
     const int G = row_attn_heads_per_wave(a.H, a.Hkv);
-    gx = sat_mul(a.rows, a.P, ceil_div(a.H / G, kDecodeWaves));
+    gx = a.mode == 3 ? sat_mul(a.rows, a.H / G) : sat_mul(a.rows, a.P, ceil_div(a.H / G, kDecodeWaves));
   }
   if (gx <= 0) return HS_OK;
   if (gx > 0x7fffffffLL)

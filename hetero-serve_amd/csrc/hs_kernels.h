@@ -21,7 +21,8 @@ struct RowAttnArgs {
   int rows;               // rows in the grid (>= real rows when cu_q is set)
   int S;                  // rows per sequence when cu_q is null
   int B, H, Hkv, BS, MB, NB;
-  int mode;               // 0 one pass, 1 fixed partitions, 2 num_splits slices
+  int mode;               // 0 one pass, 1 fixed partitions, 2 num_splits slices,
+                          // 3 one pass per workgroup, keys split over its waves
   int part_tokens;        // mode 1
   int splits;             // mode 2
   int P;                  // partition slots per (row, head) in the grid

@@ -116,7 +116,12 @@ size_t hs_decode_workspace_bytes(int B, int H, int Hkv, int D, int BS, int MB, i
  *                     ceil(ctx_b / num_splits) tokens, then an
  *                     log-sum-exp merge                            (v3)
  *                0  = fixed partitions of partition_tokens tokens
- *                     plus the merge (the fast default)
+ *                     plus the merge (the fast default; with
+ *                     partition_tokens == 0, a small grid of rows of at most
+ *                     1024 keys by the table's width instead runs one
+ *                     workgroup per (sequence, head group) whose waves split
+ *                     the keys and merge in LDS: no merge launch, the
+ *                     workspace unused)
  *   partition_tokens  used when num_splits == 0; 0 = library default (512
  *                tokens, fewer for GQA groups and for grids of fewer than 4
  *                waves per CU; fp16 and bf16 caches with 2 or more query

@@ -239,10 +239,12 @@ def test_split_invariance_and_partition_sizes():
 
 
 def test_small_grid_default_partition():
-    """With the library's default decomposition a small batch gets shorter
-    partitions (more waves on the CUs): C1's 8 x 12 rows with a 512-token
-    table run 32-token partitions (16 per row, the workspace says so), and the
-    result agrees with explicit 512-token partitions and the oracle."""
+    """With the library's default decomposition a small batch gets more waves
+    on the CUs: the workspace query for C1's 8 x 12 rows with a 512-token
+    table reports 32-token partitions (16 per row); the call itself, whose
+    rows fit one workgroup, splits each row over a workgroup's waves instead
+    (no merge).  The result agrees with explicit 512-token partitions and the
+    oracle."""
     from heteroserve import _hip
 
     _mods()
@@ -261,6 +263,38 @@ def test_small_grid_default_partition():
     fixed = _hip.decode(q, kp, vp, bt, ctx, scale, 0, partition_tokens=512)
     assert _maxerr(got, _oracle(q, kp, vp, bt, ctx, scale)) <= 2e-3
     assert _maxerr(got, fixed) <= 1e-4
+
+
+@pytest.mark.parametrize("H,Hkv,D,dtype", [
+    (12, 12, 64, torch.float16),    # C1's geometry: 16 waves per workgroup
+    (8, 8, 128, torch.bfloat16),
+    (8, 4, 64, torch.float32),      # G = 2
+    (16, 4, 128, torch.float32),    # G = 4
+    (16, 2, 64, torch.float32),     # G = 8: 8 waves per workgroup
+    (4, 4, 256, torch.float16),     # head dim 256: 8 waves per workgroup
+    (6, 2, 32, torch.float32),      # 3 query heads per KV head (one per wave), head dim 32
+])
+def test_workgroup_split_decode(H, Hkv, D, dtype):
+    """Small grids of short rows (the default decomposition, up to 1024 keys
+    by the table's width, where the VALU kernel runs): one workgroup per
+    (row, head group) splits the row's keys over its waves and merges their
+    states in LDS.  Rows of 0, 1, 7 and 9 tokens (empty and ragged slices,
+    a zero row), full rows and every length between, against the oracle and
+    explicit 64-token partitions, twice (bit-identical)."""
+    from heteroserve import _hip
+
+    _mods()
+    lens = [0, 1, 7, 9, 16, 100, 255, 333, 512, 700, 1000, 1024]
+    pool, q, bt, ctx = _random_case(lens, H, Hkv, D, 16, dtype, seed=52)
+    kp, vp = pool[0, 0], pool[0, 1]
+    scale = D ** -0.5
+    got = _hip.decode(q, kp, vp, bt, ctx, scale, 0)
+    want = _oracle(q, kp, vp, bt, ctx, scale)
+    assert _maxerr(got[1:], want[1:]) <= 1e-4
+    assert torch.count_nonzero(got[0]) == 0                       # context 0: a zero row
+    part = _hip.decode(q, kp, vp, bt, ctx, scale, 0, partition_tokens=64)
+    assert _maxerr(got, part) <= 1e-5
+    assert torch.equal(got, _hip.decode(q, kp, vp, bt, ctx, scale, 0))
 
 
 @pytest.mark.parametrize("H,Hkv,D,dtype,lens", [
