@@ -72,7 +72,7 @@ LEG_KERNELS = {
     "C2": ("hs::row_attn_part_kernel<hs::Bf16, 128, true, 1>", 16384, "C2 alone"),
     "C3": ("hs::row_attn_part_kernel<hs::Bf16, 128, true, 1>", 32640, "every leg"),
     "B64-4k": ("hs::row_attn_part_kernel<hs::Bf16, 128, true, 1>", 8192, "every leg"),
-    "C1": ("hs::row_attn_part_kernel<_Float16, 64, true, 1>", None, "every leg"),
+    "C1": ("hs::row_attn_wg_kernel<_Float16, 64, true, 1, 16>", None, "every leg"),
     "C2-gqa": ("hs::splitmm_part_kernel<hs::Bf16Ops, 128, true, 4>", None, "every leg"),
     "C4": ("hs::prefill_mfma_kernel<hs::Bf16, 128, 8>", 1536, "every leg"),
     "C5_pack": ("hs::page_copy_kernel<false, true>", None, "every leg"),
@@ -861,7 +861,7 @@ def main() -> int:
 
     secondary = {}
     if not args.no_secondary:
-        legs = [("C1", "row_attn_part_kernel<_Float16, 64, true, 1>", True, 0),
+        legs = [("C1", "row_attn_wg_kernel<_Float16, 64, true, 1, 16>", True, 0),
                 ("C3", "row_attn_part_kernel<Bf16, 128, true, 1>", False, 4),
                 ("B64-4k", "row_attn_part_kernel<Bf16, 128, true, 1>", False, 8),
                 ("C2-gqa", "splitmm_part_kernel<Bf16Ops, 128, true, 4>", False, 16)]
