@@ -101,8 +101,8 @@ struct DecodePlan {
 // 384 or 256 tokens) applies there.
 //
 // Small grids: the partition is halved (down to 32 tokens, or one page per
-// wave, and never below that floor) while the launch, estimated from the table's width, has fewer than 4
-// waves per CU.  Each wave then walks a few iterations instead of a long
+// wave, and never below that floor) while the launch, estimated from the
+// table's width, has fewer than 4 waves per CU.  Each wave then walks a few iterations instead of a long
 // serial chain.  Measured on C1 (8 sequences, 12 heads, contexts up to 512):
 // 20.1 us per step at 512 tokens, 14.8 at 64, 14.3 at 32, 15.8 at 16 (the
 // merge grows).
@@ -143,10 +143,10 @@ constexpr int64_t kWgSplitMaxTokens = 1024;
 // The default decomposition of a small grid whose rows are short: instead of
 // partitions cut down to a few tokens and a merge launch, one workgroup per
 // (row, head group) splits the row's keys over its waves and combines their
-// states in LDS (mode 3; no workspace).  Applies where the VALU kernel runs
-// and the partition above was shortened for the grid.  Measured on C1 (8
-// sequences, 12 heads, head dim 64, fp16, up to 512 tokens): step 14.3 us
-// with 32-token partitions and the merge.
+// states in LDS (mode 3; the caller's workspace goes unused).  Applies where
+// the VALU kernel runs and the partition above was shortened for the grid.
+// Measured on C1 (8 sequences, 12 heads, head dim 64, fp16, up to 512
+// tokens): step 14.3 us with 32-token partitions and the merge, 12.6 us so.
 static bool wg_split_applies(int B, int H, int Hkv, int BS, int MB, int kv_dtype, int D) {
   if (splitmm_serves(kv_dtype, BS, D, H, Hkv)) return false;
   if ((int64_t)MB * BS > kWgSplitMaxTokens) return false;
