@@ -102,10 +102,10 @@ struct DecodePlan {
 //
 // Small grids: the partition is halved (down to 32 tokens, or one page per
 // wave, and never below that floor) while the launch, estimated from the
-// table's width, has fewer than 4 waves per CU.  Each wave then walks a few iterations instead of a long
-// serial chain.  Measured on C1 (8 sequences, 12 heads, contexts up to 512):
-// 20.1 us per step at 512 tokens, 14.8 at 64, 14.3 at 32, 15.8 at 16 (the
-// merge grows).
+// table's width, has fewer than 4 waves per CU.  Each wave then walks a few
+// iterations instead of a long serial chain.  Measured on C1 (8 sequences, 12
+// heads, contexts up to 512): 20.1 us per step at 512 tokens, 14.8 at 64, 14.3
+// at 32, 15.8 at 16 (the merge grows).
 static int shrink_for_small_grid(int pt, int min_pt, int64_t waves_per_part, int BS, int MB) {
   int dev = 0;
   const int cus = hipGetDevice(&dev) == hipSuccess ? device_cu_count(dev) : 0;

@@ -260,7 +260,8 @@ template <typename T, int D, int G>
 static void launch_wg(const RowAttnArgs& a, hipStream_t stream) {
   constexpr int W = wg_waves(G, D);
   const int tpl = 64 / (D / Elem<T>::kVec);
-  const dim3 grid((unsigned)((int64_t)a.rows * (a.H / G))), block(W * 64);   // checked by the caller
+  // the grid size is checked by the caller
+  const dim3 grid((unsigned)((int64_t)a.rows * (a.H / G))), block(W * 64);
   if (a.BS % tpl == 0)
     hipLaunchKernelGGL((row_attn_wg_kernel<T, D, true, G, W>), grid, block, 0, stream, a);
   else
@@ -313,7 +314,8 @@ int launch_row_attn(const RowAttnArgs& a, int kv_dtype, int D, hipStream_t strea
     gx = splitmm_grid(a);
   } else {
     const int G = row_attn_heads_per_wave(a.H, a.Hkv);
-    gx = a.mode == 3 ? sat_mul(a.rows, a.H / G) : sat_mul(a.rows, a.P, ceil_div(a.H / G, kDecodeWaves));
+    gx = a.mode == 3 ? sat_mul(a.rows, a.H / G)
+                     : sat_mul(a.rows, a.P, ceil_div(a.H / G, kDecodeWaves));
   }
   if (gx <= 0) return HS_OK;
   if (gx > 0x7fffffffLL)
