@@ -729,7 +729,7 @@ def cpu_prefill_baseline(case, heads: int = 0):
         P = n - S
         flops += 4 * heads * D * (S * P + S * (S + 1) // 2)
     return {
-        "value": round(flops / total / 1e12, 4), "unit": "TFLOP/s",
+        "value": float(f"{flops / total / 1e12:.4g}"), "unit": "TFLOP/s",   # 4 significant digits
         "cores": torch.get_num_threads(), "kind": "port",
         "sample": (f"all {len(case.ctx)} {case.name} sequences, {heads} of {case.n_heads} heads, "
                    f"oracle/attention.py prefill_one (torch fp32 CPU), median of 3 after 1 "
