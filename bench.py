@@ -665,7 +665,7 @@ def cpu_decode_baseline(case, n_seq: int = 0, seed: int = 7):
     nbytes = tokens * case.row_bytes()
     what = "all" if n_pick == len(case.ctx) else f"a seeded sample of {n_pick} of the"
     return {
-        "value": round(nbytes / total / 1e9, 3),
+        "value": float(f"{nbytes / total / 1e9:.4g}"),
         "unit": "GB/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
@@ -692,7 +692,7 @@ def cpu_decode_batched(case):
     t = median_time(lambda: res.__setitem__("out", paged_attention_torch(*args, case.scale)))
     nbytes = case.decode_bytes()
     return {
-        "value": round(nbytes / t / 1e9, 3), "unit": "GB/s", "cores": torch.get_num_threads(),
+        "value": float(f"{nbytes / t / 1e9:.4g}"), "unit": "GB/s", "cores": torch.get_num_threads(),
         "kind": "port", "us_per_step": round(t * 1e6, 1),
         "sample": (f"the whole {case.name} batch ({len(case.ctx)} sequences) in one call of "
                    f"oracle/attention.py paged_attention_torch (torch fp32 CPU), median of 3 "
