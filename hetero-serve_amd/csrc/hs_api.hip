@@ -174,7 +174,11 @@ static int plan_decode(int BS, int MB, int num_splits, int partition_tokens, int
     if (pt % 16 != 0) return fail(HS_EINVAL, "partition_tokens must be a multiple of 16");
     const int64_t P = ceil_div(max_ctx, pt);
     if (P > 0x7fffffffLL) return fail(HS_EUNSUPPORTED, "too many partitions per row");
-    *plan = {P <= 1 ? 0 : 1, pt, 0, (int)(P < 1 ? 1 : P)};
+    // fixed partitions stay mode 1 when one covers the row (the partition
+    // kernel then writes the output itself, no merge): the grouped-query
+    // matrix-core kernel serves mode 1 only, and a one-pass plan sent those
+    // rows to the VALU kernel, 7-10x slower for 4 query heads per KV head
+    *plan = {1, pt, 0, (int)(P < 1 ? 1 : P)};
   }
   return HS_OK;
 }
