@@ -106,12 +106,14 @@ struct DecodePlan {
 // iterations instead of a long serial chain.  Measured on C1 (8 sequences, 12
 // heads, contexts up to 512): 20.1 us per step at 512 tokens, 14.8 at 64, 14.3
 // at 32, 15.8 at 16 (the merge grows).
-static int shrink_for_small_grid(int pt, int min_pt, int64_t waves_per_part, int BS, int MB) {
+static int shrink_for_small_grid(int pt, int min_pt, int64_t waves_per_part, int BS, int MB,
+                                 int waves_per_cu = 4) {
   int dev = 0;
   const int cus = hipGetDevice(&dev) == hipSuccess ? device_cu_count(dev) : 0;
   if (cus <= 0) return pt;
   const int64_t max_ctx = (int64_t)MB * BS;
-  while (pt > min_pt && sat_mul(waves_per_part, ceil_div(max_ctx, pt)) < 4 * (int64_t)cus)
+  while (pt > min_pt &&
+         sat_mul(waves_per_part, ceil_div(max_ctx, pt)) < waves_per_cu * (int64_t)cus)
     pt = std::max(min_pt, pt / 2);
   return pt;
 }
@@ -127,11 +129,16 @@ static int valu_partition(int H, int Hkv) {
 static int default_partition(int B, int H, int Hkv, int BS, int MB, int kv_dtype, int D) {
   const int G = H / Hkv;
   if (splitmm_serves(kv_dtype, BS, D, H, Hkv)) {
-    // split-operand matrix-core decode: splitmm_waves(G) waves share a partition
+    // split-operand matrix-core decode: splitmm_waves(G) waves share a
+    // partition.  Up to 4 query heads per KV head the cut goes on to 8 waves
+    // per CU (32 query heads, bf16, D 128, step us at 4 / 8 waves per CU:
+    // 8 KV heads, B 4: 10.9 / 9.8; B 8 at 2-4k tokens: 29.1 / 27.4; B 16 at
+    // 1-2k: 28.7 / 26.8; C2-gqa unchanged), above 4 it stays at 4 (4 KV
+    // heads, B 16 at 1-2k: 17.5 / 20.8)
     const int kw = splitmm_waves(G);
     return shrink_for_small_grid(splitmm_default_partition(G, D),
                                  std::max(kMinDefaultPartition, BS * kw),
-                                 sat_mul(B, Hkv, ceil_div(G, 16), kw), BS, MB);
+                                 sat_mul(B, Hkv, ceil_div(G, 16), kw), BS, MB, G <= 4 ? 8 : 4);
   }
   return shrink_for_small_grid(valu_partition(H, Hkv), kMinDefaultPartition,
                                sat_mul(B, Hkv, G / row_attn_heads_per_wave(H, Hkv)), BS, MB);
