@@ -127,7 +127,9 @@ size_t hs_decode_workspace_bytes(int B, int H, int Hkv, int D, int BS, int MB, i
  *                waves per CU; fp16 and bf16 caches with 2 or more query
  *                heads per KV head, head dim 64 and 128: 768 tokens up to 4
  *                heads per KV head, 384 up to 8, 256 otherwise and at head
- *                dim 32).
+ *                dim 32, cut for grids of fewer than 8 waves per CU up to 4
+ *                heads per KV head, 4 above).  A row that one partition
+ *                covers is written directly, without the merge.
  *                Must be a multiple of 16.
  *   workspace    device scratch of hs_decode_workspace_bytes(...) bytes
  *                (may be NULL when that is 0).
