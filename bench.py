@@ -67,10 +67,11 @@ TRAFFIC_PROFILE = ROOT / "profiles" / "bench_legs_trace_and_traffic.md"
 # Each leg's dominant kernel as rocprofv3 names it, its grid in workgroups
 # (None: the only grid that kernel ran with) and the profile's table that
 # holds it.  C2's launch (64 rows x 16 partitions of 512 tokens x 16 two-head
-# workgroups) shares its grid with C5's plain decode, so it is profiled alone.
+# workgroups) and C3's (16 rows x 64 partitions x 16) have the same grid, so
+# the run of every leg averages them in one row: each is profiled alone.
 LEG_KERNELS = {
     "C2": ("hs::row_attn_part_kernel<hs::Bf16, 128, true, 1>", 16384, "C2 alone"),
-    "C3": ("hs::row_attn_part_kernel<hs::Bf16, 128, true, 1>", 32640, "every leg"),
+    "C3": ("hs::row_attn_part_kernel<hs::Bf16, 128, true, 1>", 16384, "C3 alone"),
     "B64-4k": ("hs::row_attn_part_kernel<hs::Bf16, 128, true, 1>", 8192, "every leg"),
     "C1": ("hs::row_attn_wg_kernel<_Float16, 64, true, 1, 16>", None, "every leg"),
     "C2-gqa": ("hs::splitmm_part_kernel<hs::Bf16Ops, 128, true, 4>", None, "every leg"),
@@ -522,7 +523,7 @@ def tables_leg(steps: int) -> dict:
                     "the engine's per-sequence slot loop + fk[slots] = k"}
 
 
-def c5_step_leg(steps: int, warmup: int) -> dict:
+def c5_step_leg(steps: int, warmup: int, with_cpu: bool) -> dict:
     """C5 as one serving step on one stream: the prefill chunk's K/V written
     into its cache (1024 tokens at positions 2048..3071, fp32 slices of a fused
     QKV output), its causal attention on the matrix cores, the 255 decode
@@ -530,7 +531,14 @@ def c5_step_leg(steps: int, warmup: int) -> dict:
     of them sharing a 1024-token prefix: hs_decode_shared, which reads a
     partition that several sequences hold once for all of them), and the
     4096-block migration pack of the decode pool.  Returns the step time,
-    each part timed alone, and the plain hs_decode of the same batch."""
+    each part timed alone, and the plain hs_decode of the same batch.
+
+    With with_cpu, both attention outputs of the last step are checked
+    against the oracle on the pools as the step's own writes left them
+    (the engine's write-then-attend order, torch_engine.py:215-245 and
+    :294-313): the chunk's every row and head against prefill_one (B = 1,
+    the engine's call shape), every decode sequence against decode_one,
+    each timed on the host cores as that part's CPU baseline."""
     import torch
 
     from heteroserve import _hip
@@ -627,9 +635,249 @@ def c5_step_leg(steps: int, warmup: int) -> dict:
     out["parts"]["decode"]["basis"] = "unique K/V bytes (shared prefix counted once)"
     out["parts"]["decode"]["path"] = "hs_decode_shared"
     out["decode_plain_us"] = round(plain_ms * 1e3, 2)
+    # the outputs of the last timed step: the shared-page decode and the
+    # chunk prefill, on the pools after the step's writes
+    for f in (parts["decode"], parts["prefill"]):
+        _hip.check(f())
+    torch.cuda.synchronize()
+    if with_cpu:
+        pcpu, pouts = cpu_prefill_baseline(pc)
+        perr = max_err_prefill(pc, pout, pouts)
+        out["parts"]["prefill"].update(cpu_baseline=pcpu, max_abs_err=perr,
+                                       parity_sample="every row of the chunk, all heads")
+        del pouts
+        dcpu, douts = cpu_decode_baseline(dc, n_seq=0)
+        derr = max_err_decode(dout, douts)
+        out["parts"]["decode"].update(cpu_baseline=dcpu, max_abs_err=derr,
+                                      parity_sample="every sequence")
+        del douts
+        log(f"C5 step parity: prefill {perr:.2e} (cpu {pcpu['value']} TFLOP/s), "
+            f"shared-page decode {derr:.2e} (cpu {dcpu['value']} GB/s)")
     del dc, pc, pool, pack_out, qkv_p, qkv_d, ws
     torch.cuda.empty_cache()
     return out
+
+
+# ---------------------------------------------------------------------------
+# every entry point of the reference's harness (scripts/bench_kernel.py)
+# ---------------------------------------------------------------------------
+
+
+def _timed_calls(fn, iters: int) -> tuple:
+    """(host µs per call, device µs per call) over `iters` calls after one
+    warm-up call: the host clock between synchronisations, as the
+    reference's harness times (scripts/bench_kernel.py:53-60, Python and
+    allocation overhead included), and HIP events around the same calls on
+    the launch stream."""
+    import torch
+
+    from hsbench.timing import Event
+
+    stream = torch.cuda.current_stream().cuda_stream
+    fn()
+    torch.cuda.synchronize()
+    e0, e1 = Event(), Event()
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(iters):
+        fn()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    host = (time.perf_counter() - t0) / iters
+    return host * 1e6, e0.elapsed_ms(e1) / iters * 1e3
+
+
+def _entry_row(fn, want, nbytes: int, iters: int, rate_unit: str = "GB/s") -> dict:
+    """Check one entry point's output against the oracle, then time it."""
+    got = fn()
+    err = (got.detach().float().cpu() - want).abs().max().item()
+    host_us, dev_us = _timed_calls(fn, iters)
+    row = {"us_per_call": round(host_us, 2), "device_us_per_call": round(dev_us, 2),
+           "max_abs_err": float(f"{err:.3e}")}
+    if rate_unit == "GB/s":
+        row["gbs"] = round(nbytes / (host_us * 1e-6) / 1e9, 1)
+        row["hbm_frac"] = round(row["gbs"] / HBM_PEAK_GBS, 4)
+    else:
+        row["tflops"] = round(nbytes / (host_us * 1e-6) / 1e12, 2)
+        row["mfma_frac"] = round(row["tflops"] / MFMA_F16_PEAK_TFLOPS, 4)
+    return row
+
+
+def c2_entry_points(case, outs: dict, iters: int) -> dict:
+    """v2 (one pass) and v3 with the reference's choose_num_splits at C2,
+    through the drop-in functions, checked against the headline's per-sequence
+    oracle outputs (`outs`)."""
+    import torch
+
+    from heteroserve.model import paged_attn_v2, paged_attn_v3
+
+    args = (case.q, case.k_cache, case.v_cache, case.block_tables, case.context_lens,
+            case.scale)
+    B, H, _ = case.q.shape
+    splits = paged_attn_v3.choose_num_splits(B, H, case.block_tables.shape[1] * 16)
+    nbytes = case.decode_bytes()
+    res = {}
+    for key, fn in (("v2_paged_attention_v2", lambda: paged_attn_v2.paged_attention_v2(*args)),
+                    (f"v3_paged_attention_v3_choose_num_splits_{splits}",
+                     lambda: paged_attn_v3.paged_attention_v3(*args, splits))):
+        got = fn()
+        err = max_err_decode(got, outs)
+        host_us, dev_us = _timed_calls(fn, iters)
+        res[key] = {"us_per_call": round(host_us, 2), "device_us_per_call": round(dev_us, 2),
+                    "gbs": round(nbytes / (host_us * 1e-6) / 1e9, 1),
+                    "hbm_frac": round(nbytes / (host_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                    "max_abs_err": float(f"{err:.3e}")}
+        log(f"C2 {key}: {host_us:.1f} us/call, err {err:.2e}")
+    del got
+    torch.cuda.empty_cache()
+    return res
+
+
+# The reference's published decode rows (README :332-346, :423-430): one
+# layer of GPT-2 shape (ModelConfig(): 12 heads, head dim 64), fp16 KV,
+# block_size 16, every context at the same length, on one T4.
+REF_SHAPES = ((16, 512, 16, 128), (32, 2048, 64, 512))   # (B, ctx, published splits, prefill S)
+REF_SWEEP_SPLITS = (1, 2, 4, 8, 16, 32, 64)
+
+
+def reference_harness_leg(with_cpu: bool, iters: int = 50) -> dict:
+    """scripts/bench_kernel.py on MI355X: for each published shape, the
+    gather controls (gather + dense attention, gather + PyTorch SDPA), v1,
+    v2, v3 with choose_num_splits and v3 at the published split count, each
+    through its drop-in Python function, checked against the oracle
+    (paged_attention_torch on the CPU, same inputs) and timed as the
+    reference times them; the v3 split sweep at B16/ctx512; and the prefill
+    half (--prefill S: the scalar and the matrix-core kernel at chunk S of
+    the same contexts, against prefill_one per sequence).  Inputs as the
+    harness makes them: N(0, 1) K/V and queries, scale 1/8, a pool of
+    B * (ctx / 16 + 4) blocks; the tables here are a seeded permutation
+    (scattered pages) rather than the allocator's order."""
+    import numpy as np
+    import torch
+
+    from heteroserve.kv import pack
+    from heteroserve.model import (paged_attn, paged_attn_prefill, paged_attn_v2,
+                                   paged_attn_v3, paged_attn_wmma)
+    from hsbench import cases
+    from oracle.attention import paged_attention_torch, prefill_one
+
+    dev = "cuda:0"
+    torch.set_num_threads(host_threads())
+    res = {}
+    for B, ctx, pub_splits, S in REF_SHAPES:
+        name = f"B{B}_ctx{ctx}"
+        case = cases.build_decode(name, np.full(B, ctx), 12, 12, 64, max(64, B * (ctx // 16 + 4)),
+                                  torch.float16, dev, seed=60 + B)
+        args = (case.q, case.k_cache, case.v_cache, case.block_tables, case.context_lens,
+                case.scale)
+        host = [t.cpu() for t in args[:5]]
+        want = paged_attention_torch(*host, case.scale)
+        nbytes = case.decode_bytes()
+        splits = paged_attn_v3.choose_num_splits(B, 12, case.block_tables.shape[1] * 16)
+
+        def gather_dense():
+            ks, vs = pack.gather_kv_batch(case.pool, case.tables, ctx, 0)
+            sc = torch.einsum("bhd,bkhd->bhk", case.q, ks.float()) * case.scale
+            return torch.einsum("bhk,bkhd->bhd", torch.softmax(sc, -1), vs.float())
+
+        def gather_sdpa():
+            ks, vs = pack.gather_kv_batch(case.pool, case.tables, ctx, 0)
+            o = torch.nn.functional.scaled_dot_product_attention(
+                case.q.unsqueeze(2), ks.permute(0, 2, 1, 3).float().contiguous(),
+                vs.permute(0, 2, 1, 3).float().contiguous(), scale=case.scale)
+            return o.squeeze(2)
+
+        entries = [
+            ("gather + dense attention (control)", gather_dense),
+            ("gather + PyTorch SDPA (control)", gather_sdpa),
+            ("v1 paged_attention", lambda: paged_attn.paged_attention(*args)),
+            ("v2 paged_attention_v2", lambda: paged_attn_v2.paged_attention_v2(*args)),
+            (f"v3 paged_attention_v3, choose_num_splits = {splits}",
+             lambda: paged_attn_v3.paged_attention_v3(*args, splits)),
+        ]
+        if pub_splits != splits:
+            entries.append((f"v3 paged_attention_v3, {pub_splits} splits (the published row)",
+                            lambda: paged_attn_v3.paged_attention_v3(*args, pub_splits)))
+        rows = {}
+        for label, fn in entries:
+            rows[label] = _entry_row(fn, want, nbytes, iters)
+        shape = {"batch": B, "context": ctx, "heads": 12, "head_dim": 64, "kv_dtype": "float16",
+                 "bytes_per_call": nbytes, "rows": rows}
+        if with_cpu:
+            t = median_time(lambda: paged_attention_torch(*host, case.scale))
+            shape["cpu_baseline"] = {
+                "value": float(f"{nbytes / t / 1e9:.4g}"), "unit": "GB/s",
+                "cores": torch.get_num_threads(), "kind": "port",
+                "sample": (f"the whole batch in one call of oracle/attention.py "
+                           f"paged_attention_torch (torch fp32 CPU), median of 3 after 1 "
+                           f"warm-up: {t * 1e3:.2f} ms; cpu={cpu_model()}")}
+        if B == 16:
+            sweep = {}
+            for sp in REF_SWEEP_SPLITS:
+                sweep[str(sp)] = _entry_row(
+                    lambda sp=sp: paged_attn_v3.paged_attention_v3(*args, sp), want, nbytes, iters)
+            shape["v3_split_sweep"] = sweep
+        res[f"decode_{name}"] = shape
+        log(f"reference shapes, decode {name}: " + ", ".join(
+            f"{k.split(' (')[0]} {v['us_per_call']:.1f} us" for k, v in rows.items()))
+
+        # --prefill S: S query rows at the end of every context
+        q4 = torch.randn((B, S, 12, 64), generator=torch.Generator(device=dev).manual_seed(B),
+                         device=dev)
+        pargs = (q4, case.k_cache, case.v_cache, case.block_tables, case.context_lens,
+                 case.scale)
+        qh = q4.cpu()
+        kh, vh = host[1], host[2]
+        pwant = torch.stack([prefill_one(qh[b], kh, vh, host[3][b], ctx, case.scale)
+                             for b in range(B)])
+        flops = 4 * 12 * 64 * B * (S * (ctx - S) + S * (S + 1) // 2)
+        prows = {
+            "prefill kernel (scalar fused), paged_attention_prefill": _entry_row(
+                lambda: paged_attn_prefill.paged_attention_prefill(*pargs), pwant, flops,
+                max(5, iters // 3), "TFLOP/s"),
+            "prefill kernel (matrix cores), paged_attention_prefill_wmma": _entry_row(
+                lambda: paged_attn_wmma.paged_attention_prefill_wmma(*pargs), pwant, flops,
+                max(5, iters // 3), "TFLOP/s"),
+        }
+        res[f"prefill_{name}_S{S}"] = {"batch": B, "context": ctx, "chunk": S,
+                                       "useful_flops": flops, "rows": prows}
+        log(f"reference shapes, prefill {name} S{S}: " + ", ".join(
+            f"{k.split(',')[0]} {v['us_per_call']:.1f} us" for k, v in prows.items()))
+        del case, args, host, q4, pargs
+        torch.cuda.empty_cache()
+    return res
+
+
+def gqa_one_partition_leg(iters: int = 20) -> dict:
+    """Rows that one default partition covers, on the grouped-query path: 64
+    sequences of 100..700 tokens, 32 query heads on 8 KV heads, D 128, bf16.
+    The default decomposition keeps them on the split-operand matrix-core
+    kernel at one partition per row; v2 (one pass) runs the VALU kernel.
+    Both checked against the oracle, then timed."""
+    import numpy as np
+    import torch
+
+    from heteroserve.model import paged_attn, paged_attn_v2
+    from hsbench import cases
+    from oracle.attention import paged_attention_torch
+
+    rng = np.random.default_rng(5)
+    lens = rng.integers(100, 700, size=64, endpoint=True)
+    case = cases.build_decode("gqa-one-partition", lens, 32, 8, 128, 4096, torch.bfloat16,
+                              "cuda:0", seed=5)
+    args = (case.q, case.k_cache, case.v_cache, case.block_tables, case.context_lens,
+            case.scale)
+    want = paged_attention_torch(*[t.cpu() for t in args[:5]], case.scale)
+    nbytes = case.decode_bytes()
+    res = {"default (matrix cores, one partition a row)": _entry_row(
+               lambda: paged_attn.paged_attention(*args), want, nbytes, iters),
+           "v2 one pass (VALU)": _entry_row(
+               lambda: paged_attn_v2.paged_attention_v2(*args), want, nbytes, iters)}
+    log("GQA one-partition rows: " + ", ".join(
+        f"{k.split(' (')[0]} {v['device_us_per_call']:.1f} us" for k, v in res.items()))
+    del case, args
+    torch.cuda.empty_cache()
+    return res
 
 
 # ---------------------------------------------------------------------------
@@ -853,6 +1101,10 @@ def main() -> int:
         errors[case.name] = max_err_decode(dec["out"], outs)
         log(f"cpu baseline: {cpu['value']} GB/s on {cpu['cores']} threads; "
             f"max abs err {errors[case.name]:.2e}")
+        if not args.no_secondary and args.config == "C2":
+            c2_entries = c2_entry_points(case, outs, max(10, args.steps // 2))
+            for k, v in c2_entries.items():
+                errors[f"C2_{k}"] = v["max_abs_err"]
         del outs
     config = decode_config(case, args.partition)
     headline_name = case.name
@@ -860,6 +1112,8 @@ def main() -> int:
     torch.cuda.empty_cache()
 
     secondary = {}
+    if not args.no_secondary and with_cpu and args.config == "C2":
+        secondary["C2_entry_points"] = c2_entries
     if not args.no_secondary:
         legs = [("C1", "row_attn_wg_kernel<_Float16, 64, true, 1, 16>", True, 0),
                 ("C3", "row_attn_part_kernel<Bf16, 128, true, 1>", False, 4),
@@ -896,7 +1150,23 @@ def main() -> int:
             secondary["C4_prefill"]["parity_sample"] = "every row of every sequence, all heads"
             log(f"C4 prefill cpu baseline: {pcpu['value']} TFLOP/s; "
                 f"max abs err {errors['C4']:.2e}")
-            del pouts
+            # the scalar entry point (paged_attention_prefill's fp32 row
+            # kernel) on the same batch, against the same oracle outputs
+            from heteroserve import _hip as _h
+            sargs = (pc.q, pc.cu_seqlens, int(pc.q_lens.max()), pc.k_cache, pc.v_cache,
+                     pc.block_tables, pc.context_lens, pc.scale, False)
+            sout = _h.prefill_varlen(*sargs)
+            serr = max_err_prefill(pc, sout, pouts)
+            host_us, dev_us = _timed_calls(lambda: _h.prefill_varlen(*sargs), 5)
+            secondary["C4_prefill_scalar"] = {
+                "us_per_call": round(host_us, 2), "device_us_per_call": round(dev_us, 2),
+                "tflops": round(pre["flops"] / (dev_us * 1e-6) / 1e12, 3),
+                "max_abs_err": float(f"{serr:.3e}"),
+                "path": "hs_prefill_varlen(use_mfma=0): the fp32 row kernel of "
+                        "paged_attention_prefill"}
+            errors["C4_scalar"] = serr
+            log(f"C4 scalar prefill: {dev_us:.1f} us, err {serr:.2e}")
+            del pouts, sout
         del pc, pre
         torch.cuda.empty_cache()
 
@@ -922,8 +1192,22 @@ def main() -> int:
         exact["C5_tables"] = tb["bit_exact"]
         log(f"C5 tables + slots + KV write (B=255): {tb['us_per_step']:.1f} us, reference torch "
             f"path {tb['reference_torch_us']:.1f} us, exact={tb['bit_exact']}")
-        st = c5_step_leg(max(10, args.steps // 5), 10)
+        if with_cpu:
+            rh = reference_harness_leg(with_cpu)
+            secondary["reference_harness"] = rh
+            for shape, r in rh.items():
+                for label, row in list(r["rows"].items()) + list(
+                        r.get("v3_split_sweep", {}).items()):
+                    errors[f"{shape}: {label}"] = row["max_abs_err"]
+            g1 = gqa_one_partition_leg()
+            secondary["gqa_one_partition"] = g1
+            for label, row in g1.items():
+                errors[f"gqa_one_partition: {label}"] = row["max_abs_err"]
+        st = c5_step_leg(max(10, args.steps // 5), 10, with_cpu)
         secondary["C5_step"] = st
+        for part, key in (("prefill", "C5_step_prefill"), ("decode", "C5_step_decode")):
+            if "max_abs_err" in st["parts"][part]:
+                errors[key] = st["parts"][part]["max_abs_err"]
         log("C5 step: " + f"{st['us_per_step']:.1f} us = " + ", ".join(
             f"{k} {v['us']:.1f} us" for k, v in st["parts"].items())
             + f" (plain hs_decode: {st['decode_plain_us']:.1f} us)")

@@ -418,8 +418,20 @@ int hs_decode_noalloc(const float* q, const void* k_cache, const void* v_cache, 
                       int num_blocks, const int32_t* block_tables, const int32_t* context_lens,
                       float* out, int B, int H, int Hkv, int D, int BS, int MB, float scale,
                       int num_splits, int partition_tokens, void* stream) {
-  const size_t need = hs_decode_workspace_bytes(B, H, Hkv, D, BS, MB, num_splits,
-                                                partition_tokens);
+  // the partition states this call needs, planned for its own cache dtype
+  // (hs_decode_workspace_bytes takes none and sizes for the worst dtype)
+  size_t need = 0;
+  if (B > 0 && H > 0 && Hkv > 0 && H % Hkv == 0 && D > 0 && BS > 0 && MB > 0 &&
+      valid_dtype(kv_dtype)) {
+    DecodePlan plan;
+    const int rc = plan_decode(BS, MB, num_splits, partition_tokens,
+                               default_partition(B, H, Hkv, BS, MB, kv_dtype, D), &plan);
+    if (rc != HS_OK) return rc;
+    const int64_t n = decode_ws_bytes(B, H, D, plan.P);
+    if (n == kTooLarge)
+      return fail(HS_EUNSUPPORTED, "decode partition states too large for these sizes");
+    need = (size_t)n;
+  }
   if (need > (size_t)HS_NOALLOC_SCRATCH_BYTES)
     return fail(HS_EWORKSPACE, "hs_decode_noalloc: this call needs " + std::to_string(need) +
                                    " bytes of partition state, more than the library's fixed " +

@@ -2,10 +2,11 @@
 // head attend to keys [lo, hi) of one block-table row with an online softmax.
 //
 // This is the arithmetic of the VALU decode kernel (hs_decode.hip) and of the
-// VALU prefill path.  The matrix-core kernels (hs_prefill_mfma.hip,
-// hs_decode_gqa.hip) call it too, as their exact-range fallback: they feed
-// fp16 operands to the MFMAs, and a unit whose operands do not fit fp16 is
-// recomputed here from the same cache in fp32.
+// VALU prefill path.  The matrix-core prefill (hs_prefill_mfma.hip) calls it
+// too, as its exact-range fallback: it feeds fp16 operands to the MFMAs, and
+// a workgroup whose operands do not fit fp16 is recomputed here from the same
+// cache in fp32.  (The matrix-core decodes take split operands of the cache's
+// own type and need no fallback.)
 //
 // Wave layout (gfx950, wave64).  A 16-byte load holds kVec KV elements, so one
 // token's head row of D elements is spread over kLpt = D / kVec lanes, and one

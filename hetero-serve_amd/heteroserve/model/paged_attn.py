@@ -62,6 +62,7 @@ def paged_attention(q, k_cache, v_cache, block_tables, context_lens, scale,
     shared_pages (not in the reference's signature, default off): for batches
     whose sequences share cached prefix pages, read a partition that several
     sequences hold once for all of them (hs_decode_shared; same function,
-    fp16 matrix-core operands on the shared partitions)."""
+    matrix-core products with split 16-bit operands on the shared partitions,
+    fp32-grade results)."""
     return _hip.decode(q, k_cache, v_cache, block_tables, context_lens, scale, num_splits=0,
                        shared_pages=shared_pages)

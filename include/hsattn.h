@@ -88,9 +88,12 @@ int64_t hs_choose_num_splits(int64_t num_seqs, int64_t num_heads, int64_t max_co
  * The default also depends on the kv dtype, which this query does not take:
  * it returns the size for the shortest default any dtype gets, enough for
  * every dtype.
- * The default also shrinks (down to 32 tokens) for small grids, from B, MB
- * and the CU count of the current device: query the size with the device
- * that will run the call current.
+ * The default also shrinks for small grids (halved while the launch would
+ * have too few waves per CU, down to 32 tokens or one 16-token page per wave
+ * of the workgroup that shares a partition, whichever is longer: 64 tokens
+ * for the matrix-core decode up to 4 query heads per KV head), from B, MB and
+ * the CU count of the current device: query the size with the device that
+ * will run the call current.
  */
 size_t hs_decode_workspace_bytes(int B, int H, int Hkv, int D, int BS, int MB, int num_splits,
                                  int partition_tokens);
@@ -144,16 +147,18 @@ int hs_decode(const float* q, const void* k_cache, const void* v_cache, int kv_d
  * hs_decode without a workspace argument: the partition states go to a
  * scratch array of HS_NOALLOC_SCRATCH_BYTES (64 MiB) inside the library, one
  * per device, held until the process ends.  Same arguments and result as
- * hs_decode (bit for bit: same kernels, same decomposition); a call needing
- * more than the fixed size (hs_decode_workspace_bytes(...) >
- * HS_NOALLOC_SCRATCH_BYTES) fails with HS_EWORKSPACE before launching.  It
+ * hs_decode (bit for bit: same kernels, same decomposition); a call whose
+ * partition states, planned for its own kv_dtype, need more than the fixed
+ * size fails with HS_EWORKSPACE before launching.  (That need can be below
+ * hs_decode_workspace_bytes(...), which sizes for the worst dtype.)  It
  * allocates nothing: no hipMalloc, no hipFree, no allocating library call.
  * Every call on a device shares that device's scratch, so calls that overlap
  * in time on one device (two streams, two threads) race and must not be
  * issued.
  * No counterpart in the reference.  It is for callers that cannot allocate
- * device memory: code under HIP graph capture, tight serving loops,
- * harnesses that forbid allocation.
+ * device memory: code under HIP graph capture (a capture after one eager
+ * call on the device, which looks up the scratch address, replays bit for
+ * bit), tight serving loops, harnesses that forbid allocation.
  */
 #define HS_NOALLOC_SCRATCH_BYTES (64u << 20)
 int hs_decode_noalloc(const float* q, const void* k_cache, const void* v_cache, int kv_dtype,

@@ -92,18 +92,71 @@ def test_noalloc_matches_hs_decode_twice(H, Hkv, D, dtype):
     assert torch.equal(got, want)
 
 
-def test_noalloc_refuses_calls_beyond_its_scratch():
-    """512 sequences of up to 8192 tokens at 32 heads need 136 MB of partition
-    states, more than the fixed 64 MiB: HS_EWORKSPACE, nothing launched."""
+def test_noalloc_sizes_for_the_calls_own_cache_dtype():
+    """A bf16 cache with 4 query heads per KV head decodes on the split-operand
+    matrix cores, whose default partition is 768 tokens: 64 sequences over a
+    16384-token table need 22 partitions, ~23 MB of states.  The dtype-free
+    workspace query sizes for the VALU kernel's 256-token partitions (64
+    partitions, ~68 MB, above the fixed 64 MiB), so the call must be planned
+    for its own dtype to be accepted; it must then equal hs_decode."""
     from heteroserve import _hip
 
     lib = _hip.lib()
-    assert lib.hs_decode_workspace_bytes(512, 32, 32, 128, 16, 512, 0, 0) > (64 << 20)
-    q, kc, vc, bt, ctx = _case([16], 32, 32, 128, torch.bfloat16, seed=1)
-    out = torch.zeros((512, 32, 128), device=DEV)
+    assert lib.hs_decode_workspace_bytes(64, 32, 8, 128, 16, 1024, 0, 0) > (64 << 20)
+    lens = [16384, 5, 3000, 700, 16, 9000] + [int(x) for x in
+                                              np.random.default_rng(3).integers(1, 400, 58)]
+    case = _case(lens, 32, 8, 128, torch.bfloat16, seed=9)
+    want, got, _ = _both(case)
+    assert torch.equal(got, want)
+
+
+def test_noalloc_under_graph_capture():
+    """Captured into a HIP graph (after one eager call, which looks up the
+    scratch address) and replayed three times with eager work in between:
+    every replay equals the eager hs_decode result bit for bit."""
+    from heteroserve import _hip
+
+    lib = _hip.lib()
+    q, kc, vc, bt, ctx = _case([3000, 17, 900, 5000], 32, 8, 128, torch.bfloat16, seed=21)
+    want, _, _ = _both((q, kc, vc, bt, ctx))
+    out, head = _args(q, kc, vc, bt, ctx, 0)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        _hip.check(lib.hs_decode_noalloc(*head, side.cuda_stream))
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        _hip.check(lib.hs_decode_noalloc(*head, torch.cuda.current_stream().cuda_stream))
+    for i in range(3):
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), f"replay {i}"
+
+
+def test_noalloc_refuses_calls_beyond_its_scratch():
+    """512 sequences of up to 8192 tokens at 32 heads need 136 MB of partition
+    states, more than the fixed 64 MiB: HS_EWORKSPACE, nothing launched.  The
+    inputs have the declared sizes, so that a regression of the check fails
+    on the assertions rather than reading past the tensors."""
+    from heteroserve import _hip
+
+    lib = _hip.lib()
+    B, H, D, MB = 512, 32, 128, 512
+    assert lib.hs_decode_workspace_bytes(B, H, H, D, 16, MB, 0, 0) > (64 << 20)
+    gen = torch.Generator(device=DEV).manual_seed(1)
+    kc = torch.randn((1, 16, H, D), generator=gen, device=DEV).to(torch.bfloat16)
+    vc = torch.randn((1, 16, H, D), generator=gen, device=DEV).to(torch.bfloat16)
+    q = torch.randn((B, H, D), generator=gen, device=DEV)
+    bt = torch.zeros((B, MB), dtype=torch.int32, device=DEV)      # every page is block 0
+    ctx = torch.full((B,), MB * 16, dtype=torch.int32, device=DEV)
+    out = torch.zeros((B, H, D), device=DEV)
     rc = lib.hs_decode_noalloc(q.data_ptr(), kc.data_ptr(), vc.data_ptr(), 2, kc.shape[0],
-                               bt.data_ptr(), ctx.data_ptr(), out.data_ptr(), 512, 32, 32, 128,
-                               16, 512, 0.1, 0, 0, torch.cuda.current_stream().cuda_stream)
+                               bt.data_ptr(), ctx.data_ptr(), out.data_ptr(), B, H, H, D,
+                               16, MB, 0.1, 0, 0, torch.cuda.current_stream().cuda_stream)
     assert rc == -4
     assert b"fixed" in lib.hs_last_error()
     torch.cuda.synchronize()
