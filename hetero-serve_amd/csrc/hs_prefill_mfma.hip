@@ -716,6 +716,550 @@ void prefill_mfma_kernel(PrefillArgs a) {
                       o[d][4 * g + 3] * inv);
 }
 
+// ---------------------------------------------------------------------------
+// Pipelined kernel: 8 waves of 32 query rows, head dim 64 and 128.
+//
+// Per 64-key tile and SIMD the two resident waves issue 2 x 32 MFMAs (2048
+// cycles of the matrix pipe); everything else has to fit beside them.  Three
+// choices keep it there:
+//  * V is stored d-major in LDS (V^T, one 64-key row per dim), transposed by
+//    the producer while it widens bf16 to fp16 (the same instruction count
+//    as the widening alone), so every MFMA fragment is one ds_read_b128;
+//  * every wave moves one eighth of each tile (the keys of half a page, K and
+//    V), so no wave carries the producer alone;
+//  * three LDS buffers: while tile t is consumed, tile t+1 is complete and
+//    tile t+2 is being written.  Each wave runs a software pipeline over its
+//    32-key blocks, S^T of block b+1 (including the first block of the next
+//    tile) on the MFMA pipe beside the softmax of block b, and P.V of block b
+//    beside its producer share.
+// The softmax subtracts the running max inside the QK product (the
+// accumulator starts at -m, a register block kept per wave), and replaces
+// the per-block row max by a check of the block's probability sum: a block
+// whose fp16 probabilities could exceed 65504 (a new max more than ~15
+// above m, in log2 units) takes a rare path that raises m, rescales O and
+// redoes the block.  So a steady-state block costs 16 exponentials, 8
+// conversions and 8 dot products per lane.
+// ---------------------------------------------------------------------------
+
+constexpr int kPipeWaves = 8;
+constexpr int kPipeBufs = 3;
+constexpr float kPMax = 65504.0f;            // largest finite fp16
+
+// One tile in LDS.  K rows as in PrefillTileLds (row r of a 32-key block holds
+// key swap23(r)); V^T row d holds V[key][d] of the tile's 64 keys in key
+// order, its 16-byte chunk c (keys 8c .. 8c+7) stored at chunk
+// c ^ vt_swz<D>(d).  Layouts measured on gfx950 with the LDS bank-conflict
+// counter (ds_read_b128 / ds_write_b128, every row stride from 128 to 384
+// bytes against several chunk swizzles): for the fragment reads (32
+// consecutive rows, one chunk per lane half) and the producer's writes (rows
+// 2l, 2l + 1 of lane l at D 128; row l at D 64) both to be conflict-free,
+// D 128 takes unpadded 128-byte rows with the chunk XORed by (d >> 1) & 7,
+// and D 64 144-byte rows with no swizzle.
+template <int D>
+constexpr int vt_pad() { return D == 128 ? 0 : 8; }
+template <int D>
+__device__ inline int vt_swz(int d) { return D == 128 ? (d >> 1) & 7 : 0; }
+
+template <int D>
+struct PipeTile {
+  _Float16 k[kBN][D + kKPad];
+  _Float16 vt[D][kBN + vt_pad<D>()];
+};
+
+// The producer share of wave w: the keys 8w .. 8w+7 of each tile (half of
+// page w / 2), K and V.  V: lane l loads the D / 64 dims kVD * l .. of each of
+// the 8 keys (one coalesced token row per load instruction), widens and
+// transposes them into kVD V^T rows of 8 keys (one 16-byte LDS write each).
+// K: 16-byte chunks, kKC lanes per token row, kKU chunks per lane, written
+// row by row.  The page base is wave-uniform (one block id per wave and tile).
+template <typename T, int D>
+struct PipeProducer {
+  static constexpr int kVD = D / 64;
+  static constexpr int kKC = D / 8;
+  static constexpr int kKU = kKC / 8;
+  static constexpr int kKeysPerKU = 64 / kKC;
+  static_assert(kVD >= 1 && kKU >= 1, "head dim 64 or 128");
+
+  uint32_t v[8];      // V words of the tile in flight: key u in v[u]
+  uint4 k[kKU];       // K chunks of the tile in flight
+  int ids;            // lanes 0..3 (mod 4): block ids of the 4 pages of one tile
+  const char* kpage;  // K page of the tile whose V load_v issued (wave-uniform)
+  float chk;          // range check of the converted K words (bf16 caches)
+
+  int64_t page_bytes;  // bytes of one page of the cache
+  uint32_t v_off;      // byte offset of this lane's V word in its page (key 0 of the wave)
+  uint32_t k_off;      // byte offset of this lane's K chunk (u = 0)
+  uint32_t tok_bytes;  // bytes between consecutive tokens of a page
+  int wave, lane;
+
+  __device__ inline void init(const PrefillArgs& a, int wave_, int kvh) {
+    wave = wave_;
+    lane = threadIdx.x & 63;
+    chk = 0.0f;
+    tok_bytes = (uint32_t)(a.Hkv * D * (int)sizeof(T));
+    page_bytes = (int64_t)tok_bytes * 16;
+    const uint32_t head = (uint32_t)(kvh * D * (int)sizeof(T));
+    const uint32_t tok0 = (uint32_t)(8 * (wave & 1));
+    v_off = tok0 * tok_bytes + head + (uint32_t)(kVD * lane * (int)sizeof(T));
+    k_off = (tok0 + (uint32_t)(lane / kKC)) * tok_bytes + head +
+            (uint32_t)(8 * (lane % kKC) * (int)sizeof(T));
+  }
+
+  // Block ids of tile `tile` (clamped to the table, which has mb >= 1
+  // entries; a part without tiles asks for tile -1): one vector load.
+  __device__ inline void fetch_ids(const int32_t* bt, int mb, int tile) {
+    ids = bt[min(max(tile * 4 + (lane & 3), 0), mb - 1)];
+  }
+
+  __device__ inline const char* page(const PrefillArgs& a, const void* base) const {
+    const int id = __builtin_amdgcn_readlane(ids, wave >> 1);
+    return reinterpret_cast<const char*>(base) + safe_block(id, a.NB) * page_bytes;
+  }
+
+  // V of the tile whose ids are in `ids`; also keeps that tile's K page, so
+  // that `ids` can take the next tile's ids before load_k
+  __device__ inline void load_v(const PrefillArgs& a) {
+    kpage = page(a, a.k);
+    const char* p = page(a, a.v) + v_off;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      if constexpr (kVD == 2) {
+        v[u] = *reinterpret_cast<const uint32_t*>(p + u * tok_bytes);
+      } else {
+        v[u] = *reinterpret_cast<const uint16_t*>(p + u * tok_bytes);
+      }
+    }
+  }
+
+  __device__ inline void load_k() {
+    const char* p = kpage + k_off;
+#pragma unroll
+    for (int u = 0; u < kKU; ++u) k[u] = load16(p + u * kKeysPerKU * tok_bytes);
+  }
+
+  // fp16 word of keys (u, u+1) of dim e (0: low half of the loaded word)
+  __device__ inline uint32_t vpair(int u, int e) const {
+    if constexpr (std::is_same_v<T, Bf16>) {
+      const float x0 = __uint_as_float(e ? (v[u] & 0xffff0000u) : (v[u] << 16));
+      const float x1 = __uint_as_float(e ? (v[u + 1] & 0xffff0000u) : (v[u + 1] << 16));
+      return pack_f16(x0, x1);
+    } else {
+      return e ? __builtin_amdgcn_perm(v[u + 1], v[u], 0x07060302u)
+               : __builtin_amdgcn_perm(v[u + 1], v[u], 0x05040100u);
+    }
+  }
+
+  __device__ inline void store_v(PipeTile<D>& t) const {
+#pragma unroll
+    for (int e = 0; e < kVD; ++e) {
+      const int d = kVD * lane + e;
+      const uint4 w = make_uint4(vpair(0, e), vpair(2, e), vpair(4, e), vpair(6, e));
+      *reinterpret_cast<uint4*>(&t.vt[d][8 * (wave ^ vt_swz<D>(d))]) = w;
+    }
+  }
+
+  __device__ inline void store_k(PipeTile<D>& t) {
+#pragma unroll
+    for (int u = 0; u < kKU; ++u) {
+      const int key = 8 * wave + kKeysPerKU * u + lane / kKC;
+      const int row = (key & ~31) | swap_bits23(key & 31);
+      const uint4 h = to_f16x8<T>(k[u]);
+      if constexpr (std::is_same_v<T, Bf16>) {
+        chk = f16_check(h, chk);
+        asm volatile("" : "+v"(chk));
+      }
+      *reinterpret_cast<uint4*>(&t.k[row][8 * (lane % kKC)]) = h;
+    }
+  }
+};
+
+template <typename T, int D>
+__global__ __launch_bounds__(kPipeWaves * 64) __attribute__((amdgpu_waves_per_eu(2)))
+void prefill_pipe_kernel(PrefillArgs a) {
+  constexpr int kBM = kPipeWaves * kRowsPerWave;
+  constexpr int kDC16 = D / 16;   // QK MFMA k-steps
+  constexpr int kDB = D / 32;     // 32-dim output blocks
+  using Prod = PipeProducer<T, D>;
+  __shared__ PipeTile<D> lds[kPipeBufs];
+  __shared__ int range_fail;
+
+  // ---- which (sequence, head, query tile) -------------------------------
+  int b, h, qt, row0, S_b, ctx_b, part = 0;
+  if (a.ranked) {
+    __shared__ RankScratch rank_scratch;
+    if (!ranked_tile<kBM>(a, rank_scratch, b, h, qt, part)) return;
+    row0 = rank_scratch.row0[b];
+    S_b = rank_scratch.rows[b];
+    ctx_b = rank_scratch.ctx[b];
+  } else {
+    const int xcd = blockIdx.x % kXcds;
+    const int slot = blockIdx.x / kXcds;
+    const int pair = (slot / a.n_qt) * kXcds + xcd;
+    if (pair >= a.B * a.H) return;
+    qt = a.n_qt - 1 - slot % a.n_qt;
+    b = pair / a.H;
+    h = pair - b * a.H;
+    if (a.cu_q) {
+      row0 = a.cu_q[b];
+      S_b = a.cu_q[b + 1] - row0;
+    } else {
+      row0 = b * a.S;
+      S_b = a.S;
+    }
+    ctx_b = a.ctx[b];
+  }
+  if (qt * kBM >= S_b) return;
+  if (threadIdx.x == 0) range_fail = 0;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int j = lane & 31;
+  const int hh = lane >> 5;
+  const int kvh = h / (a.H / a.Hkv);
+  const int cap = a.MB * 16;
+  const int base_pos = ctx_b - S_b;
+
+  const int w_first = qt * kBM + wave * kRowsPerWave;
+  const int i_row = w_first + j;
+  const bool row_ok = i_row < S_b;
+  const int lim = row_ok ? min(base_pos + i_row, cap - 1) : -1;
+  const int last_row = min(qt * kBM + kBM, S_b) - 1;
+  const int kend = min(cap, base_pos + last_row + 1);
+  const int kt_all = kend > 0 ? (kend + kBN - 1) / kBN : 0;
+  const int kt_seq = (max(0, min(cap, ctx_b)) + kBN - 1) / kBN;
+  const int per_part = (kt_seq + a.n_split - 1) / a.n_split;
+  const int kt0 = min(kt_all, part * per_part);
+  const int kt1 = min(kt_all, kt0 + per_part);
+  const int n_kt = kt1 - kt0;
+  const int pg0 = min(kt0, (a.MB - 1) / (kBN / 16)) * (kBN / 16);
+  const int32_t* bt = a.bt + (int64_t)b * a.MB + pg0;
+  const int mb = a.MB - pg0;
+  const int key_base = kt0 * kBN;
+  const int w_lim_min = min(base_pos + w_first, cap - 1);
+  const int w_lim_max = w_first < S_b ? min(base_pos + min(w_first + kRowsPerWave, S_b) - 1,
+                                            cap - 1)
+                                      : -1;
+  // this wave's live 32-key blocks of the part (wave-uniform); blocks from
+  // `mask_from` on reach past the wave's first row and need the causal mask
+  const int nb_w = w_lim_max < key_base ? 0 : min(2 * n_kt, (w_lim_max - key_base) / 32 + 1);
+  const int mask_x = w_lim_min - key_base - 31;
+  const int mask_from = mask_x < 0 ? 0 : mask_x / 32 + 1;
+  const int t_w = (nb_w + 1) / 2;   // tiles with compute
+
+  // ---- prologue: Q^T fragments, tiles 0 and 1 into buffers 0 and 1, tile
+  // 2 in flight.  Tiles 0 and 1 load through two register sets at once, so
+  // the prologue pays two memory round trips (ids, then K/V), not four.
+  half8 qf[kDC16];
+  float qchk = 0.0f;
+  Prod pr, pr1;
+  pr.init(a, wave, kvh);
+  pr1 = pr;
+  pr.fetch_ids(bt, mb, 0);
+  pr1.fetch_ids(bt, mb, min(1, n_kt - 1));
+  {
+    float4 x[2 * kDC16];
+    const float* qp = a.q + ((int64_t)(row0 + min(i_row, S_b - 1)) * a.H + h) * D + 8 * hh;
+#pragma unroll
+    for (int c = 0; c < kDC16; ++c) {
+      x[2 * c] = *reinterpret_cast<const float4*>(qp + 16 * c);
+      x[2 * c + 1] = *reinterpret_cast<const float4*>(qp + 16 * c + 4);
+    }
+    pr.load_v(a);
+    pr.load_k();
+    pr1.load_v(a);
+    pr1.load_k();
+    pr.fetch_ids(bt, mb, min(2, n_kt - 1));
+    const float sc = row_ok ? a.qscale : 0.0f;
+#pragma unroll
+    for (int c = 0; c < kDC16; ++c) {
+      const float4 x0 = x[2 * c], x1 = x[2 * c + 1];
+      const uint4 w = make_uint4(pack_f16(x0.x * sc, x0.y * sc), pack_f16(x0.z * sc, x0.w * sc),
+                                 pack_f16(x1.x * sc, x1.y * sc), pack_f16(x1.z * sc, x1.w * sc));
+      qchk = f16_check(w, qchk);
+      qf[c] = __builtin_bit_cast(half8, w);
+    }
+  }
+  pr.store_v(lds[0]);
+  pr.store_k(lds[0]);
+  pr1.store_v(lds[1]);
+  pr1.store_k(lds[1]);
+  pr.chk += pr1.chk;
+  pr.load_v(a);
+  pr.fetch_ids(bt, mb, min(3, n_kt - 1));
+  pr.load_k();
+  __syncthreads();
+
+  float16x o[kDB];
+#pragma unroll
+  for (int d = 0; d < kDB; ++d)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[d][r] = 0.0f;
+  float m = kNegBig;    // running max (lanes j and j + 32 agree)
+  float l = 0.0f;       // this lane's share of the running sum
+  float16x bias;        // -m in every register: the QK accumulator's start
+  float16x s_cur, s_nxt;
+  half8 kf[kDC16];      // K fragments of the next QK block
+  half8 vf[2][kDB];     // V^T fragments of the next P.V block
+  half8 p[2];           // probabilities of the block in P.V
+
+  auto read_k = [&](const PipeTile<D>& t, int kb) __attribute__((always_inline)) {
+#pragma unroll
+    for (int c = 0; c < kDC16; ++c)
+      kf[c] = *reinterpret_cast<const half8*>(&t.k[kb * 32 + j][16 * c + 8 * hh]);
+  };
+  // accumulator register r of half hh holds key key0 + 16 (r / 8) + 8 hh + r % 8
+  auto mask = [&](float16x& s, int blk) __attribute__((always_inline)) {
+    const int key0 = key_base + 32 * blk;
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+      if (key0 + 16 * (r >> 3) + 8 * hh + (r & 7) > lim) s[r] = -INFINITY;
+  };
+  const int vsw = hh ^ vt_swz<D>(j);   // this lane's chunk swizzle (the same for rows 32 db + j)
+  // V^T fragment i (16-key chunk i / kDB, dims 32 (i % kDB) ..) of block kb
+  auto read_v1 = [&](const PipeTile<D>& t, int kb, int i) __attribute__((always_inline)) {
+    vf[i / kDB][i % kDB] = *reinterpret_cast<const half8*>(
+        &t.vt[32 * (i % kDB) + j][8 * ((4 * kb + 2 * (i / kDB)) ^ vsw)]);
+  };
+  // probabilities of pair i (registers 2i, 2i+1) of s; returns the running
+  // block sum
+  auto prob2 = [&](const float16x& s, int i, uint32_t* w, float lb) __attribute__((always_inline)) {
+    w[i] = pack_f16(fast_exp2(s[2 * i]), fast_exp2(s[2 * i + 1]));
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(half2x, w[i]),
+                                  (half2x){(_Float16)1.0f, (_Float16)1.0f}, lb, false);
+  };
+  auto probs = [&](const float16x& s) __attribute__((always_inline)) {
+    uint32_t w[8];
+    float lb = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) lb = prob2(s, i, w, lb);
+    p[0] = __builtin_bit_cast(half8, make_uint4(w[0], w[1], w[2], w[3]));
+    p[1] = __builtin_bit_cast(half8, make_uint4(w[4], w[5], w[6], w[7]));
+    return lb;
+  };
+  // One QK/softmax phase: S of the next block (when kQk) on the MFMA pipe,
+  // the probabilities of `sm` on the VALU, the V^T fragments of block `vkb`
+  // of `tv` from LDS, in that interleave: pair i of the softmax and V
+  // fragment i follow QK k-step i.
+  auto phase_qs = [&](auto qk_tag, float16x& s_out, const float16x& sm, const PipeTile<D>& tv,
+                      int vkb) __attribute__((always_inline)) {
+    constexpr bool kQk = decltype(qk_tag)::value;
+    uint32_t w[8];
+    float lb = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if constexpr (kQk) {
+        if (i < kDC16)
+          s_out = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[i], qf[i], i == 0 ? bias : s_out, 0,
+                                                         0, 0);
+      }
+      if (i < 2 * kDB) read_v1(tv, vkb, i);
+      lb = prob2(sm, i, w, lb);
+    }
+    p[0] = __builtin_bit_cast(half8, make_uint4(w[0], w[1], w[2], w[3]));
+    p[1] = __builtin_bit_cast(half8, make_uint4(w[4], w[5], w[6], w[7]));
+    if constexpr (kQk) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // LDS read
+        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);   // VALU
+      }
+    }
+    return lb;
+  };
+  // the rare path after a softmax: some probability of block s could leave
+  // fp16.  Raise m by the block's max above it, rescale O, l and the bias,
+  // shift s and (when already computed) the next block's scores, and redo
+  // the probabilities.
+  auto settle = [&](float lb, float16x& s, float16x& nxt, bool has_nxt) __attribute__((always_inline)) {
+    if (__builtin_amdgcn_ballot_w64(!(lb <= kPMax)) != 0) {
+      float mx = s[0];
+#pragma unroll
+      for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[r]);
+      mx = max_halves(mx);
+      const float dlt = mx > 0.0f ? mx : 0.0f;
+      const float corr = fast_exp2(-dlt);
+      m += dlt;
+      l *= corr;
+#pragma unroll
+      for (int d = 0; d < kDB; ++d)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[d][r] *= corr;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        bias[r] -= dlt;
+        s[r] -= dlt;
+      }
+      if (has_nxt) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) nxt[r] -= dlt;
+      }
+      lb = probs(s);
+    }
+    l += lb;
+  };
+  // One P.V phase: O += V^T . P^T on the MFMA pipe, the K fragments of the
+  // next QK block (when kRead) from LDS, and the producer's share `prod`.
+  auto phase_pv = [&](auto read_tag, const PipeTile<D>& tk, int kkb, auto&& prod) __attribute__((always_inline)) {
+    constexpr bool kRead = decltype(read_tag)::value;
+#pragma unroll
+    for (int i = 0; i < 2 * kDB; ++i) {
+      o[i % kDB] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[i / kDB][i % kDB], p[i / kDB],
+                                                          o[i % kDB], 0, 0, 0);
+      if constexpr (kRead) {
+        if (i < kDC16)
+          kf[i] = *reinterpret_cast<const half8*>(&tk.k[kkb * 32 + j][16 * i + 8 * hh]);
+      }
+    }
+    prod();
+    if constexpr (kRead) {
+#pragma unroll
+      for (int i = 0; i < 2 * kDB; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);   // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);   // LDS read
+        __builtin_amdgcn_sched_group_barrier(0x002, 3, 1);   // VALU
+      }
+    }
+  };
+  using Yes = std::true_type;
+  using No = std::false_type;
+
+  // ---- the walk ------------------------------------------------------------
+  // Period t consumes tile t (buffer t % 3) and the first block of tile t+1,
+  // writes tile t+2 (loaded during period t-1) and loads tile t+3 (block ids
+  // of tile t+4 fetched between its V and K loads).  A wave with no live
+  // blocks left only produces.  Every wave runs n_kt periods, one barrier
+  // each.
+  if (t_w > 0) {
+    // first block: its max sets m and the bias
+    read_k(lds[0], 0);
+    float16x zero;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) zero[r] = 0.0f;
+    s_cur = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[0], qf[0], zero, 0, 0, 0);
+#pragma unroll
+    for (int c = 1; c < kDC16; ++c)
+      s_cur = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[c], qf[c], s_cur, 0, 0, 0);
+    if (mask_from == 0) mask(s_cur, 0);
+    float mx = s_cur[0];
+#pragma unroll
+    for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s_cur[r]);
+    m = fmaxf(kNegBig, max_halves(mx));
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      bias[r] = -m;
+      s_cur[r] -= m;
+    }
+    read_k(lds[0], 1);
+  }
+  auto prod_v = [&](PipeTile<D>& tw, int t) __attribute__((always_inline)) {
+    return [&pr, &tw, &a, bt, mb, t, n_kt]() {
+      pr.store_v(tw);
+      pr.load_v(a);
+      pr.fetch_ids(bt, mb, min(t + 4, n_kt - 1));
+    };
+  };
+  auto prod_k = [&](PipeTile<D>& tw) __attribute__((always_inline)) {
+    return [&pr, &tw]() {
+      pr.store_k(tw);
+      pr.load_k();
+    };
+  };
+  int t = 0;
+  // full periods: blocks 2t, 2t+1 and 2t+2 are live
+  for (; t + 1 < t_w; ++t) {
+    const PipeTile<D>& tc = lds[t % kPipeBufs];
+    const PipeTile<D>& tn = lds[(t + 1) % kPipeBufs];
+    PipeTile<D>& tw = lds[(t + 2) % kPipeBufs];
+    // A: S of block 2t+1 beside the softmax of block 2t
+    if (2 * t >= mask_from) mask(s_cur, 2 * t);
+    float lb = phase_qs(Yes{}, s_nxt, s_cur, tc, 0);
+    settle(lb, s_cur, s_nxt, true);
+    // B: P.V of block 2t beside the V share of tile t+2
+    phase_pv(Yes{}, tn, 0, prod_v(tw, t));
+    // C: S of block 2t+2 beside the softmax of block 2t+1
+    if (2 * t + 1 >= mask_from) mask(s_nxt, 2 * t + 1);
+    lb = phase_qs(Yes{}, s_cur, s_nxt, tc, 1);
+    settle(lb, s_nxt, s_cur, true);
+    // D: P.V of block 2t+1 beside the K share of tile t+2
+    phase_pv(Yes{}, tn, 1, prod_k(tw));
+    __syncthreads();
+  }
+  if (t < t_w) {   // the last period with compute: no QK of a next tile
+    const PipeTile<D>& tc = lds[t % kPipeBufs];
+    PipeTile<D>& tw = lds[(t + 2) % kPipeBufs];
+    const bool second = 2 * t + 1 < nb_w;
+    if (2 * t >= mask_from) mask(s_cur, 2 * t);
+    if (second) {
+      s_nxt = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[0], qf[0], bias, 0, 0, 0);
+#pragma unroll
+      for (int c = 1; c < kDC16; ++c)
+        s_nxt = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[c], qf[c], s_nxt, 0, 0, 0);
+    }
+    float lb = phase_qs(No{}, s_nxt, s_cur, tc, 0);
+    settle(lb, s_cur, s_nxt, second);
+    phase_pv(No{}, tc, 0, prod_v(tw, t));
+    if (second) {
+      if (2 * t + 1 >= mask_from) mask(s_nxt, 2 * t + 1);
+      lb = phase_qs(No{}, s_cur, s_nxt, tc, 1);
+      settle(lb, s_nxt, s_cur, false);
+      phase_pv(No{}, tc, 1, prod_k(tw));
+    } else {
+      prod_k(tw)();
+    }
+    __syncthreads();
+    ++t;
+  }
+  for (; t < n_kt; ++t) {   // producer only
+    PipeTile<D>& tw = lds[(t + 2) % kPipeBufs];
+    prod_v(tw, t)();
+    prod_k(tw)();
+    __syncthreads();
+  }
+
+  // ---- range check, normalise and store ------------------------------------
+  // fp16 operands that overflowed (a bf16 K value >= 65536 among the walked
+  // keys, a scaled query >= 65520) fail the K and Q checks; a V value that
+  // overflowed makes O infinite or NaN (0 x inf for a zero probability).
+  bool my_fail = f16_check_failed(pr.chk + qchk);
+  {
+    float oc = 0.0f;
+#pragma unroll
+    for (int d = 0; d < kDB; ++d)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) oc += o[d][r] * 0.0f;
+    my_fail = my_fail || !(oc == 0.0f);
+  }
+  if (my_fail) range_fail = 1;
+  __syncthreads();
+  if (range_fail) {
+    prefill_rows_fp32<T, D>(a, b, h, kvh, row0, S_b, base_pos, cap, w_first, kt0 * kBN,
+                            kt1 * kBN, part);
+    return;
+  }
+  const float lsum = sum_halves(l);
+  if (!row_ok) return;
+  float inv;
+  float* op;
+  if (a.n_split > 1) {
+    if (i_row >= a.rows_cap) return;
+    const int64_t pair = ((int64_t)(part * a.B + b) * a.rows_cap + i_row) * a.H + h;
+    if (hh == 0) a.part_ml[pair] = make_float2(m, lsum);
+    inv = 1.0f;
+    op = a.part_o + pair * D + 4 * hh;
+  } else {
+    inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
+    op = a.out + ((int64_t)(row0 + i_row) * a.H + h) * D + 4 * hh;
+  }
+#pragma unroll
+  for (int d = 0; d < kDB; ++d)
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+      *reinterpret_cast<float4*>(op + d * 32 + 8 * g) =
+          make_float4(o[d][4 * g] * inv, o[d][4 * g + 1] * inv, o[d][4 * g + 2] * inv,
+                      o[d][4 * g + 3] * inv);
+}
+
 // Merge of a split prefill: for row i of sequence b and head h,
 //   out = sum_p w_p O_p / sum_p w_p l_p,  w_p = exp2(m_p - max_p m_p)
 // over the n_split parts (a part without keys for the row has m_p = -3e38 and
@@ -778,7 +1322,12 @@ int launch_typed(PrefillArgs a, int max_rows_per_seq, hipStream_t stream) {
   if (sat_mul(slots, kXcds) > 0x7fffffffLL) return fail(HS_EUNSUPPORTED, "prefill grid too large");
   a.slots_per_xcd = (int)slots;
   const dim3 grid((unsigned)(kXcds * a.slots_per_xcd)), block(Shape<D, W>::kThreads);
-  hipLaunchKernelGGL((prefill_mfma_kernel<T, D, W>), grid, block, 0, stream, a);
+  // 8-wave workgroups at head dim 64 and 128 take the pipelined kernel; the
+  // 4-wave shape (small grids without a workspace, head dim 32) the other
+  if constexpr (W == kPipeWaves && D >= 64)
+    hipLaunchKernelGGL((prefill_pipe_kernel<T, D>), grid, block, 0, stream, a);
+  else
+    hipLaunchKernelGGL((prefill_mfma_kernel<T, D, W>), grid, block, 0, stream, a);
   if (a.n_split > 1) {
     // the workspace of B * rows_cap * H * (D + 2) floats per part exists, so
     // this product fits; the grid must still fit one launch
