@@ -74,7 +74,7 @@ LEG_KERNELS = {
     "C3": ("hs::row_attn_part_kernel<hs::Bf16, 128, true, 1>", 16384, "C3 alone"),
     "B64-4k": ("hs::row_attn_part_kernel<hs::Bf16, 128, true, 1>", 8192, "every leg"),
     "C1": ("hs::row_attn_wg_kernel<_Float16, 64, true, 1, 16>", None, "every leg"),
-    "C2-gqa": ("hs::splitmm_part_kernel<hs::Bf16Ops, 128, true, 4>", None, "every leg"),
+    "C2-gqa": ("hs::splitmm_even_kernel<hs::Bf16Ops, 128, true, 4>", None, "every leg"),
     "C4": ("hs::prefill_pipe_kernel<hs::Bf16, 128>", 1536, "every leg"),
     "C5_pack": ("hs::page_copy_kernel<false, true>", None, "every leg"),
     "C5_unpack": ("hs::page_copy_kernel<true, true>", None, "every leg"),
@@ -849,14 +849,16 @@ def reference_harness_leg(with_cpu: bool, iters: int = 50) -> dict:
 
 
 def gqa_one_partition_leg(iters: int = 20) -> dict:
-    """Rows that one default partition covers, on the grouped-query path: 64
+    """Rows that one fixed partition covers, on the grouped-query path: 64
     sequences of 100..700 tokens, 32 query heads on 8 KV heads, D 128, bf16.
-    The default decomposition keeps them on the split-operand matrix-core
-    kernel at one partition per row; v2 (one pass) runs the VALU kernel.
-    Both checked against the oracle, then timed."""
+    The library default (the even split: one equal range of the batch's
+    pages per workgroup) against 768-token partitions, one a row, on the
+    split-operand matrix-core kernel, and v2 (one pass), which runs the VALU
+    kernel.  Each checked against the oracle, then timed."""
     import numpy as np
     import torch
 
+    from heteroserve import _hip
     from heteroserve.model import paged_attn, paged_attn_v2
     from hsbench import cases
     from oracle.attention import paged_attention_torch
@@ -869,8 +871,10 @@ def gqa_one_partition_leg(iters: int = 20) -> dict:
             case.scale)
     want = paged_attention_torch(*[t.cpu() for t in args[:5]], case.scale)
     nbytes = case.decode_bytes()
-    res = {"default (matrix cores, one partition a row)": _entry_row(
+    res = {"default (matrix cores, even split)": _entry_row(
                lambda: paged_attn.paged_attention(*args), want, nbytes, iters),
+           "768-token partitions (matrix cores, one a row)": _entry_row(
+               lambda: _hip.decode(*args, 0, partition_tokens=768), want, nbytes, iters),
            "v2 one pass (VALU)": _entry_row(
                lambda: paged_attn_v2.paged_attention_v2(*args), want, nbytes, iters)}
     log("GQA one-partition rows: " + ", ".join(
@@ -1010,6 +1014,9 @@ def decode_config(case, partition: int) -> dict:
         "num_blocks": int(case.k_cache.shape[0]),
         "decomposition": (f"fixed partitions of {partition} tokens + LSE merge"
                           if partition else
+                          "library default: even split (all pages cut into one equal range "
+                          "per resident workgroup, then an LSE merge of the rows cut)"
+                          if case.kv_heads < case.n_heads <= 4 * case.kv_heads else
                           "library default partitions (512 tokens, halved down to 32 while "
                           "the grid has fewer than 4 waves per CU) + LSE merge"),
         "parallelism": "none (one GPU)",
@@ -1118,7 +1125,7 @@ def main() -> int:
         legs = [("C1", "row_attn_wg_kernel<_Float16, 64, true, 1, 16>", True, 0),
                 ("C3", "row_attn_part_kernel<Bf16, 128, true, 1>", False, 4),
                 ("B64-4k", "row_attn_part_kernel<Bf16, 128, true, 1>", False, 8),
-                ("C2-gqa", "splitmm_part_kernel<Bf16Ops, 128, true, 4>", False, 16)]
+                ("C2-gqa", "splitmm_even_kernel<Bf16Ops, 128, true, 4>", False, 16)]
         for name, kernel, batched, n_seq in legs:
             if name == headline_name:
                 continue

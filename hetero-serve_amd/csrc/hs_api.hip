@@ -203,6 +203,34 @@ static int64_t decode_ws_bytes(int64_t rows, int H, int D, int P) {
 // Sizes a query function cannot report (0 means "none needed" there).
 constexpr int64_t kTooLarge = INT64_MAX;
 
+// The default decomposition of the grouped-query matrix-core decode with up
+// to 4 query heads per KV head (16-bit caches, 16-token pages), on grids
+// large enough: the even split (mode 4, hs_decode_splitmm.hip), one equal
+// share of all pages per workgroup, then a merge of the rows it cut.  Calls
+// that name a partition or a split count keep those decompositions.
+static bool even_applies(int kv_dtype, int BS, int D, int B, int H, int Hkv, int MB,
+                         int num_splits, int partition_tokens) {
+  return num_splits == 0 && partition_tokens == 0 && BS == 16 &&
+         splitmm_even_groups(kv_dtype, D, H, Hkv, B, MB) > 0;
+}
+
+// Workspace bytes of a decode call with this kv dtype (checked sizes) into
+// *need, kTooLarge when they do not fit; returns the planning error, if any.
+static int decode_need(int B, int H, int Hkv, int D, int BS, int MB, int kv_dtype,
+                       int num_splits, int partition_tokens, int64_t* need) {
+  if (even_applies(kv_dtype, BS, D, B, H, Hkv, MB, num_splits, partition_tokens)) {
+    *need = splitmm_even_layout(B, H, Hkv, D,
+                                splitmm_even_groups(kv_dtype, D, H, Hkv, B, MB)).end;
+    return HS_OK;
+  }
+  DecodePlan plan;
+  const int rc = plan_decode(BS, MB, num_splits, partition_tokens,
+                             default_partition(B, H, Hkv, BS, MB, kv_dtype, D), &plan);
+  if (rc != HS_OK) return rc;
+  *need = decode_ws_bytes(B, H, D, plan.P);
+  return HS_OK;
+}
+
 }  // namespace hs
 
 using namespace hs;
@@ -251,13 +279,17 @@ int64_t hs_choose_num_splits(int64_t num_seqs, int64_t num_heads, int64_t max_co
 
 size_t hs_decode_workspace_bytes(int B, int H, int Hkv, int D, int BS, int MB, int num_splits,
                                  int partition_tokens) {
-  DecodePlan plan;
   if (B <= 0 || H <= 0 || Hkv <= 0 || H % Hkv != 0 || D <= 0 || BS <= 0 || MB <= 0) return 0;
-  if (plan_decode(BS, MB, num_splits, partition_tokens,
-                  default_partition_any_dtype(B, H, Hkv, BS, MB, D), &plan) != HS_OK)
-    return 0;
-  const int64_t need = decode_ws_bytes(B, H, D, plan.P);
-  return need == kTooLarge ? 0 : (size_t)need;
+  // the largest need of the three cache dtypes (this query takes none)
+  int64_t need = 0;
+  for (int dt : {HS_DTYPE_F32, HS_DTYPE_F16, HS_DTYPE_BF16}) {
+    int64_t n = 0;
+    if (decode_need(B, H, Hkv, D, BS, MB, dt, num_splits, partition_tokens, &n) != HS_OK ||
+        n == kTooLarge)
+      return 0;
+    need = std::max(need, n);
+  }
+  return (size_t)need;
 }
 
 }  // extern "C"
@@ -297,6 +329,43 @@ static int decode_common(const float* q, const void* k_cache, const void* v_cach
   if (!valid_row_head_dim(D))
     return fail(HS_EUNSUPPORTED, "unsupported head_dim " + std::to_string(D));
   if (B == 0) return HS_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (!shared_pages &&
+      even_applies(kv_dtype, BS, D, B, H, Hkv, MB, num_splits, partition_tokens)) {
+    const int M = splitmm_even_groups(kv_dtype, D, H, Hkv, B, MB);
+    const EvenLayout l = splitmm_even_layout(B, H, Hkv, D, M);
+    if (l.end == kTooLarge)
+      return fail(HS_EUNSUPPORTED, "decode partition states too large for these sizes");
+    if (!workspace || workspace_bytes < (size_t)l.end)
+      return fail(HS_EWORKSPACE, "decode needs " + std::to_string(l.end) +
+                                     " workspace bytes, got " +
+                                     std::to_string(workspace ? workspace_bytes : 0));
+    char* ws = static_cast<char*>(workspace);
+    RowAttnArgs a{};
+    a.q = q;
+    a.k = k_cache;
+    a.v = v_cache;
+    a.bt = block_tables;
+    a.ctx = context_lens;
+    a.out = out;
+    a.part_acc = reinterpret_cast<float*>(ws + l.acc);
+    a.part_ml = reinterpret_cast<float*>(ws + l.ml);
+    a.rows = B;
+    a.S = 1;
+    a.B = B;
+    a.H = H;
+    a.Hkv = Hkv;
+    a.BS = BS;
+    a.MB = MB;
+    a.NB = num_blocks;
+    a.mode = 4;
+    a.P = 1;
+    a.even_m = M;
+    a.even_slots = M + B;
+    a.even_min_pages = splitmm_even_min_pages();
+    a.qscale = scale * kLog2e;
+    return launch_row_attn(a, kv_dtype, D, st);
+  }
   DecodePlan plan;
   if ((rc = plan_decode(BS, MB, num_splits, partition_tokens,
                         default_partition(B, H, Hkv, BS, MB, kv_dtype, D), &plan)) != HS_OK)
@@ -332,7 +401,6 @@ static int decode_common(const float* q, const void* k_cache, const void* v_cach
   a.splits = plan.splits;
   a.P = plan.P;
   a.qscale = scale * kLog2e;
-  hipStream_t st = static_cast<hipStream_t>(stream);
   if (!shared_pages || !shared_pages_apply(a, kv_dtype, D)) {
     // the default decomposition of a small grid of short rows: one
     // workgroup per row and head group (the workspace, sized for the
@@ -423,11 +491,9 @@ int hs_decode_noalloc(const float* q, const void* k_cache, const void* v_cache, 
   size_t need = 0;
   if (B > 0 && H > 0 && Hkv > 0 && H % Hkv == 0 && D > 0 && BS > 0 && MB > 0 &&
       valid_dtype(kv_dtype)) {
-    DecodePlan plan;
-    const int rc = plan_decode(BS, MB, num_splits, partition_tokens,
-                               default_partition(B, H, Hkv, BS, MB, kv_dtype, D), &plan);
+    int64_t n = 0;
+    const int rc = decode_need(B, H, Hkv, D, BS, MB, kv_dtype, num_splits, partition_tokens, &n);
     if (rc != HS_OK) return rc;
-    const int64_t n = decode_ws_bytes(B, H, D, plan.P);
     if (n == kTooLarge)
       return fail(HS_EUNSUPPORTED, "decode partition states too large for these sizes");
     need = (size_t)n;
@@ -449,12 +515,15 @@ int hs_decode_noalloc(const float* q, const void* k_cache, const void* v_cache, 
 
 size_t hs_decode_shared_workspace_bytes(int B, int H, int Hkv, int D, int BS, int MB,
                                         int partition_tokens) {
-  const size_t base = hs_decode_workspace_bytes(B, H, Hkv, D, BS, MB, 0, partition_tokens);
-  if (base == 0) return 0;   // one partition per row: nothing to share
+  // the fixed-partition states (this entry point never takes the even
+  // split), then the plan arrays
+  if (B <= 0 || H <= 0 || Hkv <= 0 || H % Hkv != 0 || D <= 0 || BS <= 0 || MB <= 0) return 0;
   DecodePlan plan;
   if (plan_decode(BS, MB, 0, partition_tokens, default_partition_any_dtype(B, H, Hkv, BS, MB, D),
                   &plan) != HS_OK)
     return 0;
+  const int64_t base = decode_ws_bytes(B, H, D, plan.P);
+  if (base == 0 || base == kTooLarge) return 0;   // one partition per row: nothing to share
   const int pu = H / Hkv <= 32 ? share_per_unit(H, Hkv) : 1;
   const int64_t end = share_layout((int64_t)base, B, plan.P,
                                    share_unit_slots(B, pu > 0 ? pu : 1)).end;

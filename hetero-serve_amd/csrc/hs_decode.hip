@@ -308,6 +308,12 @@ static int launch_dim(const RowAttnArgs& a, int D, hipStream_t stream) {
 // waited for whole CUs to drain and finished last.
 int launch_row_attn(const RowAttnArgs& a, int kv_dtype, int D, hipStream_t stream,
                     const SharePlanArgs* shared) {
+  if (a.mode == 4) {   // even split: prep + one kernel, no merge (hs_decode_splitmm.hip)
+    const int64_t gx = sat_mul(a.Hkv, ceil_div(a.H / a.Hkv, 16), a.even_m);
+    if (gx > 0x7fffffffLL) return fail(HS_EUNSUPPORTED, "grid too large");
+    launch_splitmm_even(a, kv_dtype, D, stream);
+    return check_launch("paged attention");
+  }
   const bool splitmm = splitmm_applies(a, kv_dtype, D);
   int64_t gx;
   if (splitmm) {

@@ -69,6 +69,11 @@
 // The partition states (m, l, un-normalised acc) have the VALU kernel's
 // layout and meaning, and the same merge kernel combines them; they are
 // written through LDS so each head's D floats go out as whole 128-byte lines.
+#include <algorithm>
+#include <map>
+#include <mutex>
+#include <utility>
+
 #include "hs_kernels.h"
 
 namespace hs {
@@ -84,7 +89,8 @@ typedef float float4x __attribute__((ext_vector_type(4)));
 constexpr int kSlots = 16;         // query heads per wave (MFMA N)
 constexpr int kPage = 16;          // tokens per page (block_size)
 constexpr float kSlack = 8.0f;     // lazy-rescale slack, log2 units
-constexpr int kMaxPages = 64;      // pages of a partition: one block id per lane
+constexpr int kMaxPages = 64;      // pages of a fixed partition
+constexpr int kWindow = 64;        // block ids held at a time: one per lane
 
 // One page of K and of V, both token-major as in the cache.  Row paddings:
 // K rows are read as 16-byte MFMA fragments (row j by lane j), V rows by the
@@ -220,10 +226,15 @@ __device__ inline void page_walk(const RowAttnArgs& a, PageLds<D>& w, int kvh, i
   const int ck = lane % kDC;        // loads: chunk of the head row
   const int slot = lane / kDC;      // loads: token slot
 
-  // Block ids of the partition's pages: lane i holds page lo / 16 + i.
+  // Block ids of the range's pages, 64 at a time: lane i of idv holds page
+  // page0 + 64 win + i, and idn those of the next window, loaded one window
+  // ahead so that crossing into it waits for nothing.  (A fixed partition has
+  // at most 64 pages and never leaves window 0.)
   const int page0 = lo / kPage;
   const int npages = (hi - lo + kPage - 1) / kPage;
-  const int idv = bt[min(page0 + lane, a.MB - 1)];
+  int idv = bt[min(page0 + lane, a.MB - 1)];
+  int idn = npages > kWindow ? bt[min(page0 + kWindow + lane, a.MB - 1)] : 0;
+  int win = 0;
 
   // Q^T fragments, split: lane l holds column j's dims 32 st + 8 g .. + 7.
   // qexp: the power of two the query was multiplied by (kScaleQ), taken back
@@ -287,10 +298,17 @@ __device__ inline void page_walk(const RowAttnArgs& a, PageLds<D>& w, int kvh, i
   const uint32_t loff = (uint32_t)(slot * tok + 8 * ck) * 2u;   // bytes; < 16 * tok * 2
 
   typename W::Regs rg;
-  // Loads of page pg of the partition (pg < npages <= kMaxPages).
+  // Loads of page pg of the range (pg < npages).  A wave's pages increase by
+  // step < kWindow, so they enter the windows one at a time.
   auto load_page = [&](typename W::Regs& r, int pg) {
-    pg = min(pg, kMaxPages - 1);
-    const int64_t b0 = safe_block(__builtin_amdgcn_readlane(idv, pg), a.NB) * kPage;
+    if (pg / kWindow != win) {   // wave-uniform
+      win = pg / kWindow;
+      idv = idn;
+      idn = kWindow * (win + 1) < npages
+                ? bt[min(page0 + kWindow * (win + 1) + lane, a.MB - 1)] : 0;
+    }
+    const int64_t b0 =
+        safe_block(__builtin_amdgcn_readlane(idv, pg % kWindow), a.NB) * kPage;
     const char* kp = reinterpret_cast<const char*>(kbase + b0 * tok);
     const char* vp = reinterpret_cast<const char*>(vbase + b0 * tok);
 #pragma unroll
@@ -382,6 +400,82 @@ __device__ inline void page_walk(const RowAttnArgs& a, PageLds<D>& w, int kvh, i
   m -= Ops::kPBias;
 }
 
+// The kW wave states of one (row, key range, unit) combined into one: the
+// weight of each wave is 2^(m - M) with M the workgroup's max for the
+// column.  Lane (j, g) owns dims 16 d + 4 g .. + 3 of head j of the unit.
+// Each wave's rows go to its own page buffers (free once the walk is done),
+// weighted (and normalised when `single`: the range is the whole row); then
+// the workgroup sums the kW copies of a head row with D / 4 lanes per row and
+// writes it: to out_rows + hh * D when single, else to acc_rows + hh *
+// acc_stride floats, with (m, l) of head j at ml + 2 j * ml_stride.  Every
+// wave of the workgroup calls it (it holds barriers); the page buffers and
+// wave_m / wave_l are free again when it returns.
+template <int D, bool kCols, int kW>
+__device__ inline void write_unit_state(float4x (&o)[D / 16], float m, float l, int gc,
+                                        bool single, float* out_rows, float* acc_rows,
+                                        int64_t acc_stride, float* ml, int64_t ml_stride,
+                                        PageLds<D> (&lds)[kW], float (&wave_m)[kW][kSlots],
+                                        float (&wave_l)[kW][kSlots]) {
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  const int j = lane & 15;
+  const int g = lane >> 4;
+  float lsum = sum_across_groups(l);
+  if constexpr (kCols) {   // head j < 8: hi column j plus lo column j + 8
+#pragma unroll
+    for (int d = 0; d < D / 16; ++d)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[d][i] += dpp<kDppRowRor8>(o[d][i]);
+  }
+  float sc = 1.0f;
+  if constexpr (kW > 1) {
+    if (g == 0) {
+      wave_m[wv][j] = m;
+      wave_l[wv][j] = lsum;
+    }
+    __syncthreads();
+    float mm = wave_m[0][j];
+#pragma unroll
+    for (int w = 1; w < kW; ++w) mm = fmaxf(mm, wave_m[w][j]);
+    float ll = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kW; ++w) ll += wave_l[w][j] * fast_exp2(wave_m[w][j] - mm);
+    sc = fast_exp2(m - mm);
+    m = mm;
+    lsum = ll;
+  }
+  constexpr int kSt = D + 4;                          // floats per staged row
+  static_assert(kSlots * kSt * sizeof(float) <= sizeof(PageLds<D>), "staging fits");
+  if (single) sc *= lsum > 0.0f ? 1.0f / lsum : 0.0f;
+  float* st = reinterpret_cast<float*>(&lds[wv]);
+#pragma unroll
+  for (int d = 0; d < D / 16; ++d)
+    *reinterpret_cast<float4*>(&st[j * kSt + 16 * d + 4 * g]) =
+        make_float4(o[d][0] * sc, o[d][1] * sc, o[d][2] * sc, o[d][3] * sc);
+  if (!single && wv == 0 && g == 0 && j < gc)
+    *reinterpret_cast<float2*>(ml + 2 * (int64_t)j * ml_stride) = make_float2(m, lsum);
+  if constexpr (kW > 1) __syncthreads();
+  constexpr int kLr = D / 4;                          // lanes per head row
+  constexpr int kHp = 64 / kLr;                       // head rows per wave and pass
+  const int c4 = lane % kLr;
+  for (int hb = wv * kHp; hb < gc; hb += kW * kHp) {  // wave-uniform
+    const int hh = hb + lane / kLr;
+    if (hh < gc) {
+      float4 x = *reinterpret_cast<const float4*>(
+          &reinterpret_cast<const float*>(&lds[0])[hh * kSt + 4 * c4]);
+#pragma unroll
+      for (int w = 1; w < kW; ++w) {
+        const float4 y = *reinterpret_cast<const float4*>(
+            &reinterpret_cast<const float*>(&lds[w])[hh * kSt + 4 * c4]);
+        x = make_float4(x.x + y.x, x.y + y.y, x.z + y.z, x.w + y.w);
+      }
+      float* dst = single ? out_rows + (int64_t)hh * D : acc_rows + (int64_t)hh * acc_stride;
+      *reinterpret_cast<float4*>(dst + 4 * c4) = x;
+    }
+  }
+  __syncthreads();   // staging read by every wave before the buffers are reused
+}
+
 // One workgroup per (row, partition, KV head, head chunk): kW waves take the
 // partition's pages in turn (wave w: pages w, w + kW, ...), then combine
 // their states through LDS, so the partition writes one state however many
@@ -391,10 +485,7 @@ template <typename Ops, int D, bool kCols, int kW>
 __global__ __launch_bounds__(64 * kW) void splitmm_part_kernel(RowAttnArgs a) {
   __shared__ PageLds<D> lds[kW];
   __shared__ float wave_m[kW][kSlots], wave_l[kW][kSlots];
-  const int lane = threadIdx.x & 63;
   const int wv = threadIdx.x >> 6;
-  const int j = lane & 15;
-  const int g = lane >> 4;
   const int G = a.H / a.Hkv;
   const int n_hc = (G + kSlots - 1) / kSlots;          // head chunks per KV head
   const int n_units = a.Hkv * n_hc;
@@ -426,69 +517,227 @@ __global__ __launch_bounds__(64 * kW) void splitmm_part_kernel(RowAttnArgs a) {
   float m, l;
   page_walk<Ops, D, kCols>(a, lds[wv], kvh, gc, a.bt + (int64_t)b * a.MB, lo, hi, wv, kW, orow0,
                            o, m, l);
-  float lsum = sum_across_groups(l);
-  if constexpr (kCols) {   // head j < 8: hi column j plus lo column j + 8
+  const int64_t pi0 = ((int64_t)row * a.H + h0) * a.P + p;   // state of head h0
+  write_unit_state<D, kCols, kW>(o, m, l, gc, nparts == 1, a.out + orow0,
+                                 a.part_acc + pi0 * D, (int64_t)a.P * D, a.part_ml + 2 * pi0,
+                                 a.P, lds, wave_m, wave_l);
+}
+
+// ---------------------------------------------------------------------------
+// Even split (mode 4): the decode's pages cut into equal shares
+// ---------------------------------------------------------------------------
+//
+// A unit's work is every page of every row: with the rows' pages laid end to
+// end (row b's pages start at R_b = pages of rows 0 .. b - 1), the Tp pages
+// are cut into M ranges of Q = ceil(Tp / M) pages, one per workgroup, and M
+// workgroups per unit fill the chip about once.  A range that crosses a row
+// boundary is walked one row piece ("segment") at a time.  So every
+// workgroup reads the same number of bytes, whatever the mix of context
+// lengths, and the grid drains all at once: fixed partitions leave a last,
+// partly filled round of workgroups (C2's batch: 1816 workgroups of 768
+// tokens on 1024 slots).
+//
+// A segment that is a whole row writes the normalised output.  Otherwise it
+// writes its state to slot (unit, w + b) (w the workgroup's range, b the row:
+// distinct for every segment, M + B slots per unit), and even_merge_kernel,
+// launched next, combines the segments of each such row.  (Merging in the
+// same kernel, by the last segment to arrive, needs an agent-scope release
+// and acquire per segment to cross the XCDs' separate L2s; measured on
+// MI355X that made the C2-gqa decode 3.5x slower.)
+
+// Pages of sequence b: ceil(end / 16), end = ctx clamped to [0, MB * BS].
+__device__ inline int row_pages(const RowAttnArgs& a, int b) {
+  const int64_t cap = (int64_t)a.MB * a.BS;
+  int64_t e = a.ctx[b];
+  e = e < 0 ? 0 : (e < cap ? e : cap);
+  return (int)((e + kPage - 1) / kPage);
+}
+
+// Lane l's value of x, as a wave-uniform (scalar) value.
+__device__ inline int64_t lane_value64(int64_t x, int l) {
+  const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)x, l);
+  const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)((uint64_t)x >> 32), l);
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
+__device__ inline int64_t wave_sum64(int64_t x) {
 #pragma unroll
-    for (int d = 0; d < D / 16; ++d)
+  for (int off = 1; off < 64; off <<= 1) x += __shfl_xor(x, off);
+  return lane_value64(x, 0);
+}
+
+// Tp: the pages of all rows (each wave of the caller computes it).
+__device__ inline int64_t total_pages(const RowAttnArgs& a) {
+  const int lane = threadIdx.x & 63;
+  int64_t tp = 0;
+  for (int c = 0; c < a.B; c += 64) tp += wave_sum64(c + lane < a.B ? row_pages(a, c + lane) : 0);
+  return tp;
+}
+
+// Q, the pages of a range: Tp cut into at most even_m ranges of at least
+// even_min_pages pages (a small decode takes fewer workgroups, the rest of
+// the grid finds its range empty).
+__device__ inline int64_t range_pages(const RowAttnArgs& a, int64_t tp) {
+  const int64_t m = max((int64_t)1, min((int64_t)a.even_m,
+                                        (tp + a.even_min_pages - 1) / a.even_min_pages));
+  return max((int64_t)1, (tp + m - 1) / m);
+}
+
+template <typename Ops, int D, bool kCols, int kW>
+__global__ __launch_bounds__(64 * kW) void splitmm_even_kernel(RowAttnArgs a) {
+  __shared__ PageLds<D> lds[kW];
+  __shared__ float wave_m[kW][kSlots], wave_l[kW][kSlots];
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  const int G = a.H / a.Hkv;
+  const int n_hc = (G + kSlots - 1) / kSlots;
+  const int n_units = a.Hkv * n_hc;
+  const int kg = min(G, kSlots);                        // state rows per slot
+  const int unit = (int)(blockIdx.x % n_units);         // unit-fastest: units spread over XCDs
+  const int wr = (int)(blockIdx.x / n_units);           // this workgroup's range, < M
+  const int kvh = unit / n_hc;
+  const int hc = unit - kvh * n_hc;
+  const int h0 = kvh * G + hc * kSlots;
+  const int gc = min(kSlots, G - hc * kSlots);
+
+  // This range [s, e) and its first row r (R_r <= s < R_{r+1}); every wave
+  // computes the same (scalar) values.
+  // (The first 64 rows' pages stay in registers between the two passes.)
+  const int64_t v0 = lane < a.B ? row_pages(a, lane) : 0;
+  int64_t tp = wave_sum64(v0);
+  for (int c = 64; c < a.B; c += 64)
+    tp += wave_sum64(c + lane < a.B ? row_pages(a, c + lane) : 0);
+  const int64_t Q = range_pages(a, tp);
+  const int64_t s = (int64_t)wr * Q;
+  const int64_t e = min(s + Q, tp);
+  if (s >= e) return;                                   // workgroup-uniform
+  int r = a.B;
+  int64_t Rr = tp;
+  int64_t base = 0;
+  for (int c = 0; c < a.B; c += 64) {
+    const int64_t v = c == 0 ? v0 : (c + lane < a.B ? row_pages(a, c + lane) : 0);
+    int64_t inc = v;                                    // inclusive scan over the chunk
 #pragma unroll
-      for (int i = 0; i < 4; ++i) o[d][i] += dpp<kDppRowRor8>(o[d][i]);
-  }
-  // This wave's weight in the combined state: 2^(m - M) with M the
-  // workgroup's max for the column.
-  float sc = 1.0f;
-  if constexpr (kW > 1) {
-    if (g == 0) {
-      wave_m[wv][j] = m;
-      wave_l[wv][j] = lsum;
+    for (int off = 1; off < 64; off <<= 1) {
+      const int64_t y = __shfl_up(inc, off);
+      if (lane >= off) inc += y;
     }
-    __syncthreads();
-    float mm = wave_m[0][j];
-#pragma unroll
-    for (int w = 1; w < kW; ++w) mm = fmaxf(mm, wave_m[w][j]);
-    float ll = 0.0f;
-#pragma unroll
-    for (int w = 0; w < kW; ++w) ll += wave_l[w][j] * fast_exp2(wave_m[w][j] - mm);
-    sc = fast_exp2(m - mm);
-    m = mm;
-    lsum = ll;
+    const uint64_t hit = __builtin_amdgcn_ballot_w64(c + lane < a.B && base + inc > s);
+    if (hit != 0) {
+      const int l0 = __builtin_ctzll(hit);
+      r = c + l0;
+      Rr = base + lane_value64(inc - v, l0);
+      break;
+    }
+    base += lane_value64(inc, 63);
   }
 
-  // Lane (j, g) owns dims 16 d + 4 g .. + 3 of head h0 + j.  Each wave's
-  // rows go to its own page buffers (free now), weighted (and normalised
-  // when the partition is the whole row); then the workgroup sums the kW
-  // copies of a head row with D / 4 lanes per row and writes it out.
-  constexpr int kSt = D + 4;                          // floats per staged row
-  static_assert(kSlots * kSt * sizeof(float) <= sizeof(PageLds<D>), "staging fits");
-  const bool single = nparts == 1;
-  if (single) sc *= lsum > 0.0f ? 1.0f / lsum : 0.0f;
-  float* st = reinterpret_cast<float*>(&lds[wv]);
+  float4x o[D / 16];
+  float m, l;
+  for (; r < a.B && Rr < e; ++r) {                      // workgroup-uniform
+    const int pr = row_pages(a, r);
+    const int64_t Rn = Rr + pr;
+    if (pr > 0) {
+      const int64_t pa = max(s, Rr), pb = min(e, Rn);   // pa < pb: this row's segment
+      const int64_t cap = (int64_t)a.MB * a.BS;
+      const int end = (int)min((int64_t)a.ctx[r], cap);
+      const int lo = (int)(pa - Rr) * kPage;
+      const int hi = (int)min((pb - Rr) * kPage, (int64_t)end);
+      const int64_t orow0 = ((int64_t)r * a.H + h0) * D;
+      page_walk<Ops, D, kCols>(a, lds[wv], kvh, gc, a.bt + (int64_t)r * a.MB, lo, hi, wv, kW,
+                               orow0, o, m, l);
+      const int64_t slot = ((int64_t)unit * a.even_slots + wr + r) * kg;   // head h0's state
+      write_unit_state<D, kCols, kW>(o, m, l, gc, pa == Rr && pb == Rn, a.out + orow0,
+                                     a.part_acc + slot * D, D, a.part_ml + 2 * slot, 1, lds,
+                                     wave_m, wave_l);
+    }
+    Rr = Rn;
+  }
+}
+
+// One wave per (row, head): a row cut over several ranges gets the
+// log-sum-exp merge of its segments' states (the merge kernel's arithmetic,
+// hs_decode.hip), a row without keys a zero output; a row inside one range
+// was written by the even-split kernel.  Latency-bound (a few MB in all): one
+// pass over the context lengths gives Tp and R_r, lane p reads segment p's
+// (max, sum), and the partial outputs are read 8 segments at a time, each
+// weight taken from the lane that computed it.
+template <int D>
+__global__ __launch_bounds__(256) void even_merge_kernel(RowAttnArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t wg = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (wg >= (int64_t)a.B * a.H) return;
+  const int r = (int)(wg / a.H);
+  const int h = (int)(wg - (int64_t)r * a.H);
+  float* dst = a.out + wg * D;
+  constexpr int kPer = (D + 63) / 64;
+  int64_t tp = 0, Rr = 0;                               // all pages; pages of rows before r
+  for (int c = 0; c < a.B; c += 64) {
+    const int b = c + lane;
+    const int64_t v = b < a.B ? row_pages(a, b) : 0;
+    tp += wave_sum64(v);
+    Rr += wave_sum64(b < r ? v : 0);
+  }
+  const int pr = row_pages(a, r);
+  if (pr == 0) {
 #pragma unroll
-  for (int d = 0; d < D / 16; ++d)
-    *reinterpret_cast<float4*>(&st[j * kSt + 16 * d + 4 * g]) =
-        make_float4(o[d][0] * sc, o[d][1] * sc, o[d][2] * sc, o[d][3] * sc);
-  const int64_t pi0 = ((int64_t)row * a.H + h0) * a.P + p;   // state of head h0
-  if (!single && wv == 0 && g == 0 && j < gc)
-    *reinterpret_cast<float2*>(a.part_ml + 2 * (pi0 + (int64_t)j * a.P)) = make_float2(m, lsum);
-  if constexpr (kW > 1) __syncthreads();
-  constexpr int kLr = D / 4;                          // lanes per head row
-  constexpr int kHp = 64 / kLr;                       // head rows per wave and pass
-  const int c4 = lane % kLr;
-  for (int hb = wv * kHp; hb < gc; hb += kW * kHp) {  // wave-uniform
-    const int hh = hb + lane / kLr;
-    if (hh < gc) {
-      float4 x = *reinterpret_cast<const float4*>(
-          &reinterpret_cast<const float*>(&lds[0])[hh * kSt + 4 * c4]);
+    for (int i = 0; i < kPer; ++i)
+      if (lane + 64 * i < D) dst[lane + 64 * i] = 0.0f;
+    return;
+  }
+  const int64_t Q = range_pages(a, tp);
+  const int64_t w_first = Rr / Q, w_last = (Rr + pr - 1) / Q;
+  if (w_first == w_last) return;
+  const int G = a.H / a.Hkv;
+  const int n_hc = (G + kSlots - 1) / kSlots;
+  const int kg = min(G, kSlots);
+  const int kvh = h / G, hc = (h - kvh * G) / kSlots;
+  const int jh = h - kvh * G - hc * kSlots;             // head within its unit
+  const int64_t unit = (int64_t)kvh * n_hc + hc;
+  // segment w's state row: slot (unit, w + r), head jh
+  const int64_t s0 = (unit * a.even_slots + w_first + r) * kg + jh;
+  const int n = (int)(w_last - w_first + 1);
+  const float2* ml = reinterpret_cast<const float2*>(a.part_ml);
+  const float2 none = make_float2(kNegBig, 0.0f);
+  const float2 st0 = lane < n ? ml[s0 + (int64_t)lane * kg] : none;
+  float mm = st0.x;
+  for (int p = 64 + lane; p < n; p += 64) mm = fmaxf(mm, ml[s0 + (int64_t)p * kg].x);
 #pragma unroll
-      for (int w = 1; w < kW; ++w) {
-        const float4 y = *reinterpret_cast<const float4*>(
-            &reinterpret_cast<const float*>(&lds[w])[hh * kSt + 4 * c4]);
-        x = make_float4(x.x + y.x, x.y + y.y, x.z + y.z, x.w + y.w);
+  for (int off = 32; off >= 1; off >>= 1) mm = fmaxf(mm, __shfl_xor(mm, off));
+  constexpr int kBatch = 8;
+  float acc[kPer];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) acc[i] = 0.0f;
+  float lsum = 0.0f;
+  for (int p0 = 0; p0 < n; p0 += 64) {
+    const int nn = min(64, n - p0);
+    const float2 st = p0 == 0 ? st0 : (lane < nn ? ml[s0 + (int64_t)(p0 + lane) * kg] : none);
+    const float wt = lane < nn ? fast_exp2(st.x - mm) : 0.0f;
+    lsum = fmaf(st.y, wt, lsum);
+    const float* pa = a.part_acc + (s0 + (int64_t)p0 * kg) * D;
+    for (int p = 0; p < nn; p += kBatch) {
+      float v[kBatch][kPer];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u)
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+          const int d = lane + 64 * i;
+          v[u][i] = (p + u < nn && d < D) ? pa[(int64_t)(p + u) * kg * D + d] : 0.0f;
+        }
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const float wu = __builtin_bit_cast(
+            float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wt), min(p + u, 63)));
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) acc[i] = fmaf(v[u][i], wu, acc[i]);
       }
-      float* dst = single ? a.out + orow0 + (int64_t)hh * D
-                          : a.part_acc + (pi0 + (int64_t)hh * a.P) * D;
-      *reinterpret_cast<float4*>(dst + 4 * c4) = x;
     }
   }
+  lsum = group_sum<64>(lsum);
+  const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i)
+    if (lane + 64 * i < D) dst[lane + 64 * i] = acc[i] * inv;
 }
 
 }  // namespace
@@ -561,6 +810,117 @@ static void launch_for(const RowAttnArgs& a, int D, hipStream_t stream) {
 void launch_splitmm_part(const RowAttnArgs& a, int kv_dtype, int D, hipStream_t stream) {
   if (kv_dtype == HS_DTYPE_F16) launch_for<F16Ops>(a, D, stream);
   else launch_for<Bf16Ops>(a, D, stream);
+}
+
+// ---------------------------------------------------------------------------
+// even split: host side
+// ---------------------------------------------------------------------------
+
+// The even split serves groups of at most 4 query heads per KV head (one
+// 4-wave workgroup per unit, hi and lo terms as MFMA columns) on grids whose
+// fixed partitions would take more than one round of the device.  Measured
+// on MI355X against fixed partitions (whole call, us): C2-gqa 109 / 113, 300
+// sequences of 16..3000 tokens 328 / 378, 64 x 4096 tokens 177 / 189, C2
+// contexts at head dim 64 (fp16) 66 / 69.  It lost with 8 query heads per KV
+// head (C2 contexts, 4 KV heads: 74 / 69 at 16-page ranges, 70 / 69 at 32)
+// and where the partitions fit one round (64 rows of 100..700 tokens, one
+// 768-token partition each: 31.8 / 24.0; 8 rows of 1-4k tokens: 25.5 /
+// 24.8): there the merge launch costs more than the last round's idle slots.
+constexpr int kEvenMaxGroup = 4;
+constexpr int kEvenWaves = 4;
+// Workgroups of the device's occupancy per CU taken by the grid: filled once
+// (C2-gqa: 109 us; twice 114, three times 116), and the least pages of a
+// range (16: 4 a wave; 32 measured the same on C2-gqa).
+constexpr int kEvenRounds = 1;
+constexpr int kEvenMinPages = 16;
+
+template <typename Ops>
+static const void* even_kernel_t(int D) {
+  if (D == 32) return (const void*)splitmm_even_kernel<Ops, 32, true, kEvenWaves>;
+  if (D == 64) return (const void*)splitmm_even_kernel<Ops, 64, true, kEvenWaves>;
+  return (const void*)splitmm_even_kernel<Ops, 128, true, kEvenWaves>;
+}
+
+static const void* even_kernel(int kv_dtype, int D) {
+  return kv_dtype == HS_DTYPE_F16 ? even_kernel_t<F16Ops>(D) : even_kernel_t<Bf16Ops>(D);
+}
+
+int splitmm_even_min_pages() { return kEvenMinPages; }
+
+// Resident workgroups of the kernel per CU and the CU count, on the current
+// device; looked up once per (device, kernel).
+static void even_occupancy(const void* fn, int block, int* occ, int* cus) {
+  static std::mutex mu;
+  static std::map<std::pair<int, const void*>, std::pair<int, int>> cache;
+  int dev = 0;
+  *occ = 0;
+  *cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return;
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = cache.find({dev, fn});
+  if (it == cache.end()) {
+    int n = 0, c = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, block, 0) != hipSuccess) n = 0;
+    if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) c = 0;
+    it = cache.emplace(std::make_pair(dev, fn), std::make_pair(n, c)).first;
+  }
+  *occ = it->second.first;
+  *cus = it->second.second;
+}
+
+// M, the workgroups per unit: the device's resident workgroups (kEvenRounds
+// times over) split between the units.  0 when the even split does not
+// serve the call: more than kEvenMaxGroup query heads per KV head, or fixed
+// default partitions that fit one round (B rows of the table's width, a
+// bound on the real count, at most M partitions per unit).
+int splitmm_even_groups(int kv_dtype, int D, int H, int Hkv, int B, int MB) {
+  const int G = H / Hkv;
+  if (!splitmm_serves(kv_dtype, kPage, D, H, Hkv) || G > kEvenMaxGroup) return 0;
+  int occ = 0, cus = 0;
+  even_occupancy(even_kernel(kv_dtype, D), 64 * kEvenWaves, &occ, &cus);
+  if (occ <= 0 || cus <= 0) return 0;
+  const int64_t fill = ceil_div((int64_t)cus * occ * kEvenRounds, Hkv);
+  const int64_t parts = sat_mul(B, ceil_div((int64_t)MB * kPage, splitmm_default_partition(G, D)));
+  if (parts <= fill) return 0;
+  return (int)std::min<int64_t>(fill, 1 << 20);
+}
+
+EvenLayout splitmm_even_layout(int B, int H, int Hkv, int D, int M) {
+  const int G = H / Hkv;
+  const int64_t n_units = (int64_t)Hkv * ceil_div(G, kSlots);
+  const int64_t states = sat_mul(n_units, sat_add(M, B), std::min(G, kSlots));
+  EvenLayout l;
+  l.acc = 0;
+  l.ml = sat_add(sat_mul(states, D, (int64_t)sizeof(float)), 255) & ~(int64_t)255;
+  l.end = sat_add(l.ml, sat_mul(states, 2 * (int64_t)sizeof(float)));
+  if (l.end >= INT64_MAX - 255) l.end = INT64_MAX;
+  return l;
+}
+
+template <typename Ops>
+static void launch_even_for(const RowAttnArgs& a, int D, hipStream_t stream) {
+  const dim3 grid((unsigned)((int64_t)a.Hkv * a.even_m)), block(64 * kEvenWaves);
+  if (D == 32)
+    hipLaunchKernelGGL((splitmm_even_kernel<Ops, 32, true, kEvenWaves>), grid, block, 0, stream, a);
+  else if (D == 64)
+    hipLaunchKernelGGL((splitmm_even_kernel<Ops, 64, true, kEvenWaves>), grid, block, 0, stream, a);
+  else
+    hipLaunchKernelGGL((splitmm_even_kernel<Ops, 128, true, kEvenWaves>), grid, block, 0, stream,
+                       a);
+}
+
+// The even-split kernel, then the merge of the rows it cut (which also
+// zeroes rows without keys).  Needs a.rows == a.B (one query row per
+// sequence) and a.H / a.Hkv <= kEvenMaxGroup.
+void launch_splitmm_even(const RowAttnArgs& a, int kv_dtype, int D, hipStream_t stream) {
+  profile_begin(stream);
+  if (kv_dtype == HS_DTYPE_F16) launch_even_for<F16Ops>(a, D, stream);
+  else launch_even_for<Bf16Ops>(a, D, stream);
+  profile_end(stream);
+  const dim3 grid((unsigned)(((int64_t)a.B * a.H + 3) / 4)), block(256);
+  if (D == 32) hipLaunchKernelGGL(even_merge_kernel<32>, grid, block, 0, stream, a);
+  else if (D == 64) hipLaunchKernelGGL(even_merge_kernel<64>, grid, block, 0, stream, a);
+  else hipLaunchKernelGGL(even_merge_kernel<128>, grid, block, 0, stream, a);
 }
 
 }  // namespace hs

@@ -22,12 +22,18 @@ struct RowAttnArgs {
   int S;                  // rows per sequence when cu_q is null
   int B, H, Hkv, BS, MB, NB;
   int mode;               // 0 one pass, 1 fixed partitions, 2 num_splits slices,
-                          // 3 one pass per workgroup, keys split over its waves
+                          // 3 one pass per workgroup, keys split over its waves,
+                          // 4 even split (grouped-query matrix-core decode)
   int part_tokens;        // mode 1
   int splits;             // mode 2
   int P;                  // partition slots per (row, head) in the grid
   float qscale;           // scale * log2(e)
   const uint8_t* skip;    // [rows * P] or null: partitions the shared-page kernel serves
+  // mode 4: workgroups per unit and state slots per unit (even_m + rows);
+  // part_acc / part_ml hold the states as [unit, slot, head of the unit] rows
+  int even_m;
+  int even_slots;
+  int even_min_pages;
 };
 
 // Sequence of a row and the end of its key range (exclusive).  Returns false
@@ -110,6 +116,16 @@ int splitmm_waves(int G);                                            // waves pe
 int splitmm_default_partition(int G, int D);                         // tokens, before small-grid cuts
 int64_t splitmm_grid(const RowAttnArgs& a);
 void launch_splitmm_part(const RowAttnArgs& a, int kv_dtype, int D, hipStream_t stream);
+// Even split (mode 4) of the same kernel family: the workgroups per unit that
+// fill the device once (occupancy of the kernel that serves this geometry on
+// the current device), and the workspace its states take.
+int splitmm_even_groups(int kv_dtype, int D, int H, int Hkv, int B, int MB);   // 0: not served
+int splitmm_even_min_pages();
+struct EvenLayout {
+  int64_t acc, ml, end;   // byte offsets; end == INT64_MAX when too large
+};
+EvenLayout splitmm_even_layout(int B, int H, int Hkv, int D, int M);
+void launch_splitmm_even(const RowAttnArgs& a, int kv_dtype, int D, hipStream_t stream);
 
 // Query heads one decode wave serves (GQA packing): 1, 2, 4 or 8.
 int row_attn_heads_per_wave(int H, int Hkv);

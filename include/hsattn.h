@@ -91,9 +91,10 @@ int64_t hs_choose_num_splits(int64_t num_seqs, int64_t num_heads, int64_t max_co
  * The default also shrinks for small grids (halved while the launch would
  * have too few waves per CU, down to 32 tokens or one 16-token page per wave
  * of the workgroup that shares a partition, whichever is longer: 64 tokens
- * for the matrix-core decode up to 4 query heads per KV head), from B, MB and
- * the CU count of the current device: query the size with the device that
- * will run the call current.
+ * for the matrix-core decode up to 4 query heads per KV head), and the even
+ * split's state slots (see hs_decode) follow the kernel's occupancy, from B,
+ * MB and the CU count of the current device: query the size with the device
+ * that will run the call current.
  */
 size_t hs_decode_workspace_bytes(int B, int H, int Hkv, int D, int BS, int MB, int num_splits,
                                  int partition_tokens);
@@ -134,6 +135,15 @@ size_t hs_decode_workspace_bytes(int B, int H, int Hkv, int D, int BS, int MB, i
  *                heads per KV head, 4 above).  A row that one partition
  *                covers is written directly, without the merge.
  *                Must be a multiple of 16.
+ *                With num_splits == 0 and partition_tokens == 0, fp16 and
+ *                bf16 caches with 16-token pages and 2 to 4 query heads per
+ *                KV head take the even split instead where their default
+ *                partitions would overflow one round of the device: all
+ *                pages of the batch, rows laid end to end, cut into one
+ *                equal range per resident workgroup of each KV head, then
+ *                a merge of the rows cut across ranges.  Same function;
+ *                results agree with the fixed partitions to the
+ *                split-operand precision, not bit for bit.
  *   workspace    device scratch of hs_decode_workspace_bytes(...) bytes
  *                (may be NULL when that is 0).
  */
