@@ -851,10 +851,11 @@ def reference_harness_leg(with_cpu: bool, iters: int = 50) -> dict:
 def gqa_one_partition_leg(iters: int = 20) -> dict:
     """Rows that one fixed partition covers, on the grouped-query path: 64
     sequences of 100..700 tokens, 32 query heads on 8 KV heads, D 128, bf16.
-    The library default (the even split: one equal range of the batch's
-    pages per workgroup) against 768-token partitions, one a row, on the
-    split-operand matrix-core kernel, and v2 (one pass), which runs the VALU
-    kernel.  Each checked against the oracle, then timed."""
+    The library default (fixed partitions here: one round of the device
+    holds them, so the even split does not apply) against explicit 768-token
+    partitions, one a row, on the split-operand matrix-core kernel, and v2
+    (one pass), which runs the VALU kernel.  Each checked against the
+    oracle, then timed."""
     import numpy as np
     import torch
 
@@ -871,7 +872,7 @@ def gqa_one_partition_leg(iters: int = 20) -> dict:
             case.scale)
     want = paged_attention_torch(*[t.cpu() for t in args[:5]], case.scale)
     nbytes = case.decode_bytes()
-    res = {"default (matrix cores, even split)": _entry_row(
+    res = {"library default (matrix cores)": _entry_row(
                lambda: paged_attn.paged_attention(*args), want, nbytes, iters),
            "768-token partitions (matrix cores, one a row)": _entry_row(
                lambda: _hip.decode(*args, 0, partition_tokens=768), want, nbytes, iters),
