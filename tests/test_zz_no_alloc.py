@@ -94,9 +94,9 @@ def test_noalloc_matches_hs_decode_twice(H, Hkv, D, dtype):
 
 def test_noalloc_sizes_for_the_calls_own_cache_dtype():
     """A bf16 cache with 4 query heads per KV head decodes on the split-operand
-    matrix cores, whose default partition is 768 tokens: 64 sequences over a
-    16384-token table need 22 partitions, ~23 MB of states.  The dtype-free
-    workspace query sizes for the VALU kernel's 256-token partitions (64
+    matrix cores (64 sequences over a 16384-token table: the even split, a
+    few MB of states).  The dtype-free workspace query sizes for the worst
+    dtype, an fp32 cache on the VALU kernel's 256-token partitions (64
     partitions, ~68 MB, above the fixed 64 MiB), so the call must be planned
     for its own dtype to be accepted; it must then equal hs_decode."""
     from heteroserve import _hip
