@@ -128,15 +128,17 @@ __device__ inline E8 vt_fragment(const GqaWaveLds<D>& w, int d, int k0, int j, i
 
 // One wave's partition pass: up to 32 query slots that read the same KV
 // head and the same pages, keys [lo, hi) of block table row `bt`.  Lane
-// (j, hh) serves slot j: its query starts at element q_off of a.q.  Slots
-// j >= gc are padding (zero query, nothing written by the caller).  Returns
+// (j, hh) serves slot j: its query starts at element q_off of a.q, and it
+// sees only keys below slot_hi (a member whose context ends inside the
+// partition).  Slots j >= gc are padding (zero query, nothing written by the
+// caller).  Returns
 // the state in o / m / l in the ordinary units (m minus kPBias: o and l
 // carry the 2^kPBias factor of the probabilities); l is this lane's share of
 // the sum.
 template <typename T, int D>
 __device__ inline void gqa_wave_run(const RowAttnArgs& a, GqaWaveLds<D>& w, int lane, int kvh,
-                                    int gc, const int32_t* bt, int lo, int hi, int64_t q_off,
-                                    float16x (&o)[D / 32], float& m, float& l) {
+                                    int gc, const int32_t* bt, int lo, int hi, int slot_hi,
+                                    int64_t q_off, float16x (&o)[D / 32], float& m, float& l) {
   using Ops = Split32<T>;
   using E = typename Ops::E;
   using E8 = typename Ops::E8;
@@ -245,6 +247,7 @@ __device__ inline void gqa_wave_run(const RowAttnArgs& a, GqaWaveLds<D>& w, int 
     for (int r = 0; r < 16; ++r) o[d][r] = 0.0f;
   m = kNegBig;   // running max of slot j (shared by lanes j, j + 32)
   l = 0.0f;      // this lane's share of the running sum
+  const int lim = min(hi, slot_hi);   // this slot's keys end here
 
   load_block(0);
   for (int t0 = lo; t0 < hi; t0 += kBlock) {
@@ -269,10 +272,10 @@ __device__ inline void gqa_wave_run(const RowAttnArgs& a, GqaWaveLds<D>& w, int 
       for (int r = 0; r < 16; ++r) s[r] = ldexpf(s[r], -qexp);
     }
     // register r of half hh holds token t0 + 16 * (r / 8) + 8 * hh + r % 8
-    if (t0 + kBlock > hi) {
+    if (__builtin_amdgcn_ballot_w64(t0 + kBlock > lim) != 0) {
 #pragma unroll
       for (int r = 0; r < 16; ++r)
-        if (t0 + 16 * (r >> 3) + 8 * hh + (r & 7) >= hi) s[r] = -INFINITY;
+        if (t0 + 16 * (r >> 3) + 8 * hh + (r & 7) >= lim) s[r] = -INFINITY;
     }
     float mx = s[0];
 #pragma unroll
@@ -370,7 +373,7 @@ __device__ inline uint64_t mix64(uint64_t x) {
 constexpr int kShareSlots = 2 * kShareMaxB;   // hash-table slots (a power of two)
 
 constexpr int kPlanWaves = 16;      // waves of a plan workgroup
-constexpr int kPlanBatch = 8;       // sequences whose loads a wave issues together
+constexpr int kPlanBatch = 16;      // sequences whose loads a wave issues together
 
 // One workgroup per partition index p.  Its waves take batches of
 // kPlanBatch sequences, all of a batch's loads in flight together, the 64
@@ -380,11 +383,12 @@ constexpr int kPlanBatch = 8;       // sequences whose loads a wave issues toget
 // wave's sum of mix64(position, id).  The representative is the first
 // sequence with the same hash, found through an open-addressing table in LDS
 // and confirmed id by id (a hash collision leaves the sequence on its own).
-// Groups of at least kShareMin sequences get a range of members[] and of
-// units by atomic allocation, so the order of groups, and of sequences inside
-// a group, may differ between calls; no result depends on it (every query
-// slot of the matrix-core wave is computed on its own, its running max
-// included).
+// Sequences whose context ends inside partition p then join a group whose
+// representative holds their pages there (below).  Groups of at least
+// kShareMin full holders get a range of members[] and of units by atomic
+// allocation, so the order of groups, and of sequences inside a group, may
+// differ between calls; no result depends on it (every query slot of the
+// matrix-core wave is computed on its own, its running max included).
 __global__ __launch_bounds__(kPlanWaves * 64) void share_plan_kernel(RowAttnArgs a,
                                                                      SharePlanArgs s) {
   constexpr int kThreads = kPlanWaves * 64;
@@ -396,6 +400,8 @@ __global__ __launch_bounds__(kPlanWaves * 64) void share_plan_kernel(RowAttnArgs
   __shared__ int moff[kShareMaxB];            // representative: its members[] offset
   __shared__ int uoff[kShareMaxB];            // representative: its first unit
   __shared__ int fill[kShareMaxB];            // representative: members placed so far
+  __shared__ int fid[kShareMaxB];             // block id of the partition's first page
+  __shared__ int npart[kShareMaxB];           // pages of a partition the context ends in, else 0
   __shared__ int members_used, units_used;
   const int p = blockIdx.x;
   const int tid = threadIdx.x;
@@ -425,26 +431,40 @@ __global__ __launch_bounds__(kPlanWaves * 64) void share_plan_kernel(RowAttnArgs
       id[k] = a.bt[(int64_t)b * a.MB + col];
       ctx[k] = a.ctx[b];
     }
+    // lane k ends with the hash of sequence b0 + k, the id of its first page
+    // of the partition, and its page count there when its context ends
+    // inside the partition
+    uint64_t mine = ~0ull;
+    int my_fid = 0, my_np = 0;
 #pragma unroll
     for (int k = 0; k < kPlanBatch; ++k) {
-      const int b = b0 + k;
-      if (b >= a.B) break;                     // wave-uniform
       const int64_t end = ctx[k] < cap ? ctx[k] : cap;
-      const bool full = (int64_t)(p + 1) * a.part_tokens <= end;
+      const int64_t p_lo = (int64_t)p * a.part_tokens;
+      const bool full = p_lo + a.part_tokens <= end;
       uint64_t h = lane < pages ? mix64(((uint64_t)lane << 32) | (uint32_t)id[k]) : 0;
 #pragma unroll
       for (int off = 32; off >= 1; off >>= 1) h += __shfl_xor(h, off);
       if (!full || h == ~0ull) h = ~0ull;
-      if (lane == 0) {
-        hsh[b] = h;
-        if (h != ~0ull) {
-          // insert: claim an empty slot or find this hash's, then lower its index
-          for (int i = (int)(h & (kShareSlots - 1));; i = (i + 1) & (kShareSlots - 1)) {
-            const uint64_t old = atomicCAS(&key[i], ~0ull, h);
-            if (old == ~0ull || old == h) {
-              atomicMin(&first[i], b);
-              break;
-            }
+      const int f0 = __builtin_amdgcn_readfirstlane(id[k]);
+      if (lane == k) {
+        mine = h;
+        my_fid = f0;
+        my_np = !full && end > p_lo ? (int)((end - p_lo + 15) / 16) : 0;
+      }
+    }
+    // the batch's inserts in parallel, one lane per sequence: claim an empty
+    // slot or find this hash's, then lower its index
+    const int b = b0 + lane;
+    if (lane < kPlanBatch && b < a.B) {
+      hsh[b] = mine;
+      fid[b] = my_fid;
+      npart[b] = my_np;
+      if (mine != ~0ull) {
+        for (int i = (int)(mine & (kShareSlots - 1));; i = (i + 1) & (kShareSlots - 1)) {
+          const uint64_t old = atomicCAS(&key[i], ~0ull, mine);
+          if (old == ~0ull || old == mine) {
+            atomicMin(&first[i], b);
+            break;
           }
         }
       }
@@ -452,17 +472,21 @@ __global__ __launch_bounds__(kPlanWaves * 64) void share_plan_kernel(RowAttnArgs
   }
   __syncthreads();
   for (int b0 = wave * kPlanBatch; b0 < a.B; b0 += kPlanWaves * kPlanBatch) {
+    // lane k looks up sequence b0 + k's representative
+    int rl = -1;
+    if (lane < kPlanBatch && b0 + lane < a.B) {
+      const uint64_t h = hsh[b0 + lane];
+      if (h != ~0ull) {
+        int i = (int)(h & (kShareSlots - 1));
+        while (key[i] != h) i = (i + 1) & (kShareSlots - 1);
+        rl = first[i];
+      }
+    }
     int r[kPlanBatch], mine[kPlanBatch], other[kPlanBatch];
 #pragma unroll
     for (int k = 0; k < kPlanBatch; ++k) {
       const int b = min(b0 + k, a.B - 1);
-      const uint64_t h = hsh[b];
-      r[k] = -1;
-      if (h != ~0ull) {
-        int i = (int)(h & (kShareSlots - 1));
-        while (key[i] != h) i = (i + 1) & (kShareSlots - 1);
-        r[k] = first[i];
-      }
+      r[k] = __builtin_amdgcn_readlane(rl, k);
       mine[k] = a.bt[(int64_t)b * a.MB + col];
       other[k] = a.bt[(int64_t)max(r[k], 0) * a.MB + col];
     }
@@ -477,10 +501,73 @@ __global__ __launch_bounds__(kPlanWaves * 64) void share_plan_kernel(RowAttnArgs
   }
   __syncthreads();
   // a sequence that fell back to itself after a collision is not counted
-  // with the group of the hash's first sequence
-  for (int b = tid; b < a.B; b += kThreads) {
-    const int r = rep[b];
-    if (r >= 0 && rep[r] == r) atomicAdd(&cnt[r], 1);
+  // with the group of the hash's first sequence.  A group's members mostly
+  // share waves, so each wave adds its count per representative with one
+  // atomic (one atomic per sequence serialised on the group's counter).
+  for (int b0 = wave * 64; b0 < a.B; b0 += kThreads) {   // wave-uniform
+    const int b = b0 + lane;
+    int r = b < a.B ? rep[b] : -1;
+    if (r >= 0 && rep[r] != r) r = -1;
+    for (uint64_t todo = __builtin_amdgcn_ballot_w64(r >= 0); todo != 0;) {
+      const int rl = __builtin_amdgcn_readlane(r, __builtin_ctzll(todo));
+      const uint64_t same = __builtin_amdgcn_ballot_w64(r == rl);
+      if (lane == __builtin_ctzll(todo)) atomicAdd(&cnt[rl], __builtin_popcountll(same));
+      todo &= ~same;
+    }
+  }
+  __syncthreads();
+  // Members whose context ends inside the partition: such a sequence joins
+  // a group when its pages there are the representative's first pages (a
+  // shared prefix that the sequence has not yet grown past).  Groups are
+  // found by the id of the partition's first page (a table from that id to
+  // the group's representative, in the hash table's storage), then every
+  // page of the sequence is compared; the shared-page kernel masks each
+  // member's keys at its own context.
+  for (int i = tid; i < kShareSlots; i += kThreads) {
+    key[i] = ~0ull;
+    first[i] = 0x7fffffff;
+  }
+  __syncthreads();
+  for (int r = tid; r < a.B; r += kThreads) {
+    if (rep[r] != r || cnt[r] < kShareMin) continue;
+    const uint64_t id0 = (uint32_t)fid[r];
+    for (int i = (int)(mix64(id0) & (kShareSlots - 1));; i = (i + 1) & (kShareSlots - 1)) {
+      const uint64_t old = atomicCAS(&key[i], ~0ull, id0);
+      if (old == ~0ull || old == id0) {
+        atomicMin(&first[i], r);
+        break;
+      }
+    }
+  }
+  __syncthreads();
+  for (int b0 = wave * kPlanBatch; b0 < a.B; b0 += kPlanWaves * kPlanBatch) {
+    int rl = -1, nl = 0;                       // lane k: sequence b0 + k
+    if (lane < kPlanBatch && b0 + lane < a.B && npart[b0 + lane] > 0) {
+      const uint64_t id0 = (uint32_t)fid[b0 + lane];
+      int i = (int)(mix64(id0) & (kShareSlots - 1));
+      while (key[i] != ~0ull && key[i] != id0) i = (i + 1) & (kShareSlots - 1);
+      if (key[i] == id0) {
+        rl = first[i];
+        nl = npart[b0 + lane];
+      }
+    }
+    int r[kPlanBatch], np[kPlanBatch], mine[kPlanBatch], other[kPlanBatch];
+#pragma unroll
+    for (int k = 0; k < kPlanBatch; ++k) {
+      const int b = min(b0 + k, a.B - 1);
+      r[k] = __builtin_amdgcn_readlane(rl, k);
+      np[k] = __builtin_amdgcn_readlane(nl, k);
+      mine[k] = r[k] >= 0 ? a.bt[(int64_t)b * a.MB + col] : 0;
+      other[k] = r[k] >= 0 ? a.bt[(int64_t)r[k] * a.MB + col] : 0;
+    }
+#pragma unroll
+    for (int k = 0; k < kPlanBatch; ++k) {
+      if (r[k] < 0) continue;                  // wave-uniform
+      if (__builtin_amdgcn_ballot_w64(lane < np[k] && mine[k] != other[k]) == 0 && lane == 0) {
+        rep[b0 + k] = r[k];
+        atomicAdd(&cnt[r[k]], 1);
+      }
+    }
   }
   __syncthreads();
   for (int r = tid; r < a.B; r += kThreads) {
@@ -496,11 +583,29 @@ __global__ __launch_bounds__(kPlanWaves * 64) void share_plan_kernel(RowAttnArgs
           make_int4(off + k * s.per_unit, min(s.per_unit, n - k * s.per_unit), r, 0);
   }
   __syncthreads();
-  for (int b = tid; b < a.B; b += kThreads) {
-    const int r = rep[b];
-    const bool grouped = r >= 0 && rep[r] == r && cnt[r] >= kShareMin;
-    s.skip[(int64_t)b * a.P + p] = grouped ? 1 : 0;
-    if (grouped) s.members[(int64_t)p * a.B + moff[r] + atomicAdd(&fill[r], 1)] = b;
+  // members[]: a wave reserves its members of a group with one atomic and
+  // places them in lane order
+  for (int b0 = wave * 64; b0 < a.B; b0 += kThreads) {   // wave-uniform
+    const int b = b0 + lane;
+    int g = -1;
+    if (b < a.B) {
+      const int r = rep[b];
+      const bool grouped = r >= 0 && rep[r] == r && cnt[r] >= kShareMin;
+      s.skip[(int64_t)b * a.P + p] = grouped ? 1 : 0;
+      if (grouped) g = r;
+    }
+    for (uint64_t todo = __builtin_amdgcn_ballot_w64(g >= 0); todo != 0;) {
+      const int leader = __builtin_ctzll(todo);
+      const int rl = __builtin_amdgcn_readlane(g, leader);
+      const uint64_t same = __builtin_amdgcn_ballot_w64(g == rl);
+      int base = 0;
+      if (lane == leader) base = atomicAdd(&fill[rl], __builtin_popcountll(same));
+      base = __builtin_amdgcn_readlane(base, leader);
+      if (g == rl)
+        s.members[(int64_t)p * a.B + moff[rl] + base +
+                  __builtin_popcountll(same & ((1ull << lane) - 1))] = b;
+      todo &= ~same;
+    }
   }
   if (tid == 0) s.n_units[p] = units_used;
 }
@@ -562,8 +667,9 @@ void shared_pages_kernel(RowAttnArgs a, SharePlanArgs s) {
       const Slot t = slot_of(item);
       const int lo = t.p * a.part_tokens + wv * span;
       const int hi = wv == kGqaWaves - 1 ? (t.p + 1) * a.part_tokens : lo + span;
+      const int64_t end = a.ctx[t.mb] < cap ? a.ctx[t.mb] : cap;   // member's own keys
       gqa_wave_run<T, D>(a, lds[wv], lane, t.kvh, t.gc, a.bt + (int64_t)t.un.z * a.MB, lo, hi,
-                         t.row_h * D, o, m, l);
+                         (int)min(end, (int64_t)hi), t.row_h * D, o, m, l);
     }
     __syncthreads();   // every wave is done with its K/V tiles
     float* xs = reinterpret_cast<float*>(&lds[wv]);

@@ -182,7 +182,9 @@ int hs_decode_noalloc(const float* q, const void* k_cache, const void* v_cache, 
  * hs_decode(num_splits = 0, partition_tokens) computes.  A partition of
  * partition_tokens keys that is full in at least 4 sequences with identical
  * block ids is read once for up to 32 (sequence, head) query slots of a KV
- * head on the matrix cores (K/V as stored, q and the probabilities split
+ * head, together with the sequences whose context ends inside it on the same
+ * pages (each attending to its own keys only), on the matrix cores (K/V as
+ * stored, q and the probabilities split
  * into two 16-bit terms each, fp32 accumulation: fp32-grade results); every
  * other partition runs as in hs_decode.  The grouping is found on the device by
  * one small kernel per call.  Serves fp16/bf16 KV with BS == 16, D in

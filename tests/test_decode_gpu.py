@@ -676,10 +676,42 @@ def test_shared_pages_decode(H, Hkv, D, dtype, pt, ctx, groups):
     assert torch.equal(rev[flip], shared)
 
 
+def test_shared_pages_partial_members():
+    """Sequences whose context ends inside a shared partition (a prefix they
+    have not grown past) join the group of that partition's full holders:
+    their own keys are masked at their context, one ending in partition 0 is
+    the row's only partition (written directly), and a sequence whose pages
+    leave the shared prefix inside the partition stays on its own there.
+    Every sequence against the oracle; the call is deterministic on a rerun
+    and on the reversed batch."""
+    from heteroserve import _hip
+
+    _mods()
+    ctx = [1100, 1500, 2000, 1024, 700, 300, 900, 520, 512, 3000]
+    groups = [(range(0, 6), 64)]
+    q, kc, vc, bt, cl, scale = _shared_pages_case(ctx, groups, 8, 8, 128, torch.bfloat16, seed=77)
+    bt[6, :40] = bt[0, :40]     # 900 tokens: the prefix's first 40 pages, then its own
+    bt[7, :33] = bt[0, :33]     # 520 tokens: 33 pages, all the prefix's
+    bt[8, :32] = bt[0, :32]     # 512 tokens: partition 0 exactly
+    out = _hip.decode(q, kc, vc, bt, cl, scale, num_splits=0, partition_tokens=512,
+                      shared_pages=True)
+    want = _oracle_rows(q, kc, vc, bt, cl, scale, range(len(ctx)))
+    for b, w in want.items():
+        assert _maxerr(out[b], w) <= SPLIT_TOL[torch.bfloat16], (b, ctx[b])
+    again = _hip.decode(q, kc, vc, bt, cl, scale, num_splits=0, partition_tokens=512,
+                        shared_pages=True)
+    assert torch.equal(again, out)
+    flip = torch.arange(len(ctx) - 1, -1, -1, device=DEV)
+    rev = _hip.decode(q[flip].contiguous(), kc, vc, bt[flip].contiguous(), cl[flip].contiguous(),
+                      scale, num_splits=0, partition_tokens=512, shared_pages=True)
+    assert torch.equal(rev[flip], out)
+
+
 def test_shared_pages_c5():
-    """C5's decode batch (half the sequences share a 1024-token prefix):
-    the shared-page path against the plain (fp32 VALU) one and sampled
-    sequences against the oracle, at the bf16 split-operand tolerance."""
+    """C5's decode batch (half the sequences share a 1024-token prefix, some
+    of them ending inside it): the shared-page path against the plain (fp32
+    VALU) one, and every sequence against the oracle, at the bf16
+    split-operand tolerance."""
     from heteroserve import _hip
 
     _mods()
@@ -690,7 +722,7 @@ def test_shared_pages_c5():
     shared = _hip.decode(*args, num_splits=0, shared_pages=True)
     tol = SPLIT_TOL[case.k_cache.dtype]
     assert _maxerr(shared, plain) <= tol
-    _check_sequences(case, shared, [0, 1, 2, 3, 100, 200, 254], tol)
+    _check_sequences(case, shared, range(len(case.ctx)), tol)
     del case
     torch.cuda.empty_cache()
 
