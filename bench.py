@@ -153,7 +153,8 @@ def median_time(fn, runs: int = 3) -> float:
 # ---------------------------------------------------------------------------
 
 
-def decode_leg(case, steps: int, warmup: int, partition_tokens: int = 0) -> dict:
+def decode_leg(case, steps: int, warmup: int, partition_tokens: int = 0,
+               warm_ms: float = 0.0) -> dict:
     """Time hs_decode on `case`; returns step/kernel times, throughputs and the
     output of the last step."""
     import torch
@@ -182,7 +183,7 @@ def decode_leg(case, steps: int, warmup: int, partition_tokens: int = 0) -> dict
     def arm(s, e):
         _hip.check(lib.hs_profile_next_launch(s.handle, e.handle))
 
-    step_ms, kernel_ms, wall = time_steps(step, steps, warmup, stream, arm)
+    step_ms, kernel_ms, wall = time_steps(step, steps, warmup, stream, arm, warm_ms)
     nbytes = case.decode_bytes()
     k_ms = statistics.mean(kernel_ms)
     return dict(step_ms=step_ms, kernel_ms=k_ms, kernel_ms_min=min(kernel_ms), wall_s=wall,
@@ -1036,7 +1037,9 @@ def secondary_decode(name: str, kernel: str, steps: int, warmup: int, with_cpu: 
     from hsbench import cases
 
     case = cases.CONFIGS[name]("cuda:0")
-    dec = decode_leg(case, steps, warmup)
+    # the previous leg ended with seconds of CPU baseline: warm the clocks up
+    # (C1's 5-us steps are bound by the host's launch rate, not the clocks)
+    dec = decode_leg(case, steps, warmup, warm_ms=0.0 if name == "C1" else 50.0)
     res = {"us_per_step": round(dec["step_ms"] * 1e3, 2), "gbs": round(dec["step_gbs"], 1),
            "hbm_frac": round(dec["step_gbs"] / HBM_PEAK_GBS, 4),
            "config": decode_config(case, 0),
@@ -1097,6 +1100,11 @@ def main() -> int:
     errors = {}          # leg -> max abs error (attention legs)
     exact = {}           # leg -> bit-exact (copy legs)
 
+    # the decode legs' pools, one case at a time, in one buffer reserved as
+    # the process's first large allocation (as an engine allocates its KV
+    # pool once); the largest is C2's and B64-4k's 65536-block pool
+    arena = torch.empty(65536 * 2 * 16 * 32 * 128 * 2, dtype=torch.uint8, device=dev)
+    cases.set_pool_arena(arena)
     case = cases.CONFIGS[args.config](dev)
     log(f"{case.name}: B={len(case.ctx)} sum(ctx)={int(case.ctx.sum())} "
         f"bytes={case.decode_bytes() / 1e9:.3f} GB")
@@ -1124,9 +1132,9 @@ def main() -> int:
         secondary["C2_entry_points"] = c2_entries
     if not args.no_secondary:
         legs = [("C1", "row_attn_wg_kernel<_Float16, 64, true, 1, 16>", True, 0),
+                ("C2-gqa", "splitmm_even_kernel<Bf16Ops, 128, true, 4>", False, 16),
                 ("C3", "row_attn_part_kernel<Bf16, 128, true, 1>", False, 4),
-                ("B64-4k", "row_attn_part_kernel<Bf16, 128, true, 1>", False, 8),
-                ("C2-gqa", "splitmm_even_kernel<Bf16Ops, 128, true, 4>", False, 16)]
+                ("B64-4k", "row_attn_part_kernel<Bf16, 128, true, 1>", False, 8)]
         for name, kernel, batched, n_seq in legs:
             if name == headline_name:
                 continue
@@ -1135,7 +1143,11 @@ def main() -> int:
             secondary[f"{name}_decode"] = r
             if "max_abs_err" in r:
                 errors[name] = r["max_abs_err"]
-
+    # the other legs hold several cases at once: their own allocations
+    cases.set_pool_arena(None)
+    del arena
+    torch.cuda.empty_cache()
+    if not args.no_secondary:
         pc = cases.c4_prefill(dev)
         # >= 60 warm-up launches (~20 ms): after the memory-bound decode legs
         # the clock takes tens of milliseconds of MFMA work to ramp up

@@ -147,6 +147,33 @@ def _table_tensor(tables: list, device):
     return torch.from_numpy(bt).to(device)
 
 
+# A device buffer that decode pools are carved from, or None (each pool its
+# own allocation).  bench.py reserves it as the process's first large
+# allocation and builds its decode legs' pools in it one case at a time, as a
+# serving engine allocates its KV pool once: measured on MI355X, C2-gqa's
+# decode ran 109.7 us on a process's first pool and 112.4 us on any pool
+# allocated after a large one had been freed.
+_POOL_ARENA = None
+
+
+def set_pool_arena(buf) -> None:
+    """Carve the pools of decode cases built from now on from `buf` (a uint8
+    device tensor; None: allocate each pool).  Every build starts at the
+    buffer's beginning, so a case built from it must be deleted before the
+    next one is built."""
+    global _POOL_ARENA
+    _POOL_ARENA = buf
+
+
+def _new_pool(shape, dtype, device):
+    torch = _torch()
+    n = int(np.prod(shape)) * torch.empty((), dtype=dtype).element_size()
+    a = _POOL_ARENA
+    if a is not None and a.device == torch.device(device) and n <= a.numel():
+        return a[:n].view(dtype).view(shape)
+    return torch.empty(shape, dtype=dtype, device=device)
+
+
 def build_decode(name: str, ctx: np.ndarray, n_heads: int, kv_heads: int, head_dim: int,
                  num_blocks: int, dtype, device, seed: int, input_scale: float = 1.0,
                  rng=None, shared: Optional[list] = None,
@@ -155,8 +182,7 @@ def build_decode(name: str, ctx: np.ndarray, n_heads: int, kv_heads: int, head_d
     rng = rng if rng is not None else np.random.default_rng(seed)
     tables = _tables(rng, ctx, num_blocks, shared, share)
     gen = torch.Generator(device=device).manual_seed(seed)
-    pool = torch.empty((1, 2, num_blocks, BLOCK_SIZE, kv_heads, head_dim), dtype=dtype,
-                       device=device)
+    pool = _new_pool((1, 2, num_blocks, BLOCK_SIZE, kv_heads, head_dim), dtype, device)
     _fill_pool(pool, gen, input_scale)
     q = torch.randn((len(ctx), n_heads, head_dim), generator=gen, device=device,
                     dtype=torch.float32)

@@ -54,9 +54,12 @@ class Event:
 
 
 def time_steps(step: Callable[[], None], steps: int, warmup: int, stream: int,
-               arm: Callable[[Event, Event], None]) -> Tuple[float, List[float], float]:
-    """Run `warmup` untimed steps, then `steps` timed ones back to back, then
-    `steps` more with each step's main kernel bracketed by events.
+               arm: Callable[[Event, Event], None],
+               warm_ms: float = 0.0) -> Tuple[float, List[float], float]:
+    """Run `warmup` untimed steps (more, when they took less than `warm_ms`
+    of wall time: after a host-only phase the GPU's clocks need tens of
+    milliseconds of work to come back up), then `steps` timed ones back to
+    back, then `steps` more with each step's main kernel bracketed by events.
 
     The timed region holds the steps only: a pair of event records between
     kernels adds a few microseconds of queue work per step, so the kernel
@@ -69,9 +72,16 @@ def time_steps(step: Callable[[], None], steps: int, warmup: int, stream: int,
 
     import torch
 
+    t_w = time.perf_counter()
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
+    spent = time.perf_counter() - t_w
+    if warm_ms > 0 and spent * 1e3 < warm_ms:
+        per = spent / max(warmup, 1)
+        for _ in range(min(500, int((warm_ms * 1e-3 - spent) / max(per, 1e-6)) + 1)):
+            step()
+        torch.cuda.synchronize()
     region0, region1 = Event(), Event()
     t0 = time.perf_counter()
     region0.record(stream)
