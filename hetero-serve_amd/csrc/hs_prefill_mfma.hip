@@ -742,6 +742,9 @@ void prefill_mfma_kernel(PrefillArgs a) {
 // ---------------------------------------------------------------------------
 
 constexpr int kPipeWaves = 8;
+// Fourth word of a raw (unformatted, unswizzled) buffer resource on gfx9-family
+// GPUs, gfx950 included.
+constexpr int kBufferRsrcWord3 = 0x00020000;
 constexpr int kPipeBufs = 3;
 constexpr float kPMax = 65504.0f;            // largest finite fp16
 
@@ -816,25 +819,38 @@ struct PipeProducer {
     return reinterpret_cast<const char*>(base) + safe_block(id, a.NB) * page_bytes;
   }
 
+  // Buffer resource of one page (base, unstrided, page_bytes long): loads
+  // take the lane's offset in a VGPR and the key's in an SGPR, so a tile's
+  // loads share one 64-bit page base instead of computing an address each.
+  __device__ inline __amdgpu_buffer_rsrc_t page_rsrc(const char* page) const {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(page), (short)0,
+                                             (int)page_bytes, kBufferRsrcWord3);
+  }
+
   // V of the tile whose ids are in `ids`; also keeps that tile's K page, so
   // that `ids` can take the next tile's ids before load_k
   __device__ inline void load_v(const PrefillArgs& a) {
     kpage = page(a, a.k);
-    const char* p = page(a, a.v) + v_off;
+    const __amdgpu_buffer_rsrc_t r = page_rsrc(page(a, a.v));
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       if constexpr (kVD == 2) {
-        v[u] = *reinterpret_cast<const uint32_t*>(p + u * tok_bytes);
+        v[u] = __builtin_amdgcn_raw_buffer_load_b32(r, (int)v_off, (int)(u * tok_bytes), 0);
       } else {
-        v[u] = *reinterpret_cast<const uint16_t*>(p + u * tok_bytes);
+        v[u] = __builtin_amdgcn_raw_buffer_load_b16(r, (int)v_off, (int)(u * tok_bytes), 0);
       }
     }
   }
 
   __device__ inline void load_k() {
-    const char* p = kpage + k_off;
+    const __amdgpu_buffer_rsrc_t r = page_rsrc(kpage);
 #pragma unroll
-    for (int u = 0; u < kKU; ++u) k[u] = load16(p + u * kKeysPerKU * tok_bytes);
+    for (int u = 0; u < kKU; ++u) {
+      typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+      const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(
+          r, (int)k_off, (int)(u * kKeysPerKU * tok_bytes), 0);
+      k[u] = make_uint4(x[0], x[1], x[2], x[3]);
+    }
   }
 
   // fp16 word of keys (u, u+1) of dim e (0: low half of the loaded word)
