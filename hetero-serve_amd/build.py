@@ -64,7 +64,8 @@ COMPILE_FLAGS = [
 # iteration.  Forcing the VGPR form for MFMA operands cut the loop's
 # instruction count by ~45% (measured on the generated gfx950 code).
 PER_FILE_FLAGS = {
-    "hs_prefill_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=true"],
+    "hs_prefill_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=true",
+                            "-mllvm", "-amdgpu-atomic-optimizer-strategy=None"],
     "hs_decode_gqa.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=true"],
     "hs_decode_splitmm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=true"],
 }

@@ -160,8 +160,9 @@ int launch_prefill_mfma(const float* q, const int32_t* cu_q, int S, int max_rows
 // Launch shape of the MFMA prefill (workgroup width, key-range parts) and the
 // workspace a split needs (0 without one).
 struct PrefillPlan {
-  bool wide;     // 256-row workgroups (head dim 64 and 128)
-  int n_split;   // key-range parts per query tile (1: none)
+  bool wide;      // 256-row workgroups (head dim 64 and 128)
+  int n_split;    // key-range parts per query tile (1: none)
+  int stream_ns;  // workgroups per XCD of the persistent kernel (0: grid kernel)
 };
 PrefillPlan plan_prefill_mfma(int B, int max_rows, int H, int D, int cus, bool can_split);
 int64_t prefill_workspace_bytes(const PrefillPlan& p, int B, int max_rows, int H, int D);

@@ -54,6 +54,7 @@
 #include "hs_rowwalk.h"
 
 #include <algorithm>
+#include <cstdlib>
 #include <type_traits>
 
 namespace hs {
@@ -112,6 +113,7 @@ struct PrefillArgs {
   int rows_cap;          // query rows per sequence in the partial arrays
   float* part_o;         // [n_split, B, rows_cap, H, D]
   float2* part_ml;       // [n_split, B, rows_cap, H]
+  int* counters;         // persistent kernel: one work counter per XCD (zeroed per launch)
 };
 
 // K rows are read as 16-byte fragments (row j by lane j), V rows by the
@@ -1276,6 +1278,714 @@ void prefill_pipe_kernel(PrefillArgs a) {
                       o[d][4 * g + 3] * inv);
 }
 
+// ---------------------------------------------------------------------------
+// Persistent form of the pipelined kernel (prefill_stream_kernel): one
+// workgroup per CU takes query tiles from a per-XCD queue, and its producer
+// streams the K/V tiles of consecutive query tiles without a break.
+//
+// The grid kernel pays, for every 256-row query tile, the ranking of the
+// batch, two dependent memory round trips (block ids, then K/V) before its
+// first tile is in LDS, an epilogue and the gap until the next workgroup
+// starts on the CU: ~11 us per query tile on C4 (one tile of the key walk
+// is ~1.7 us).  Here the ranking runs once per workgroup, and the producer
+// treats the key tiles of a workgroup's consecutive query tiles as one
+// stream: while the last tiles of one query tile are consumed, the first
+// tiles of the next are already loaded, converted and stored.  The next
+// tile's Q loads are issued before the epilogue that stores the current
+// tile's output.
+//
+// Queue.  Query tiles are ranked as in the grid kernel (sequences longest
+// first, each sequence's tiles heaviest first; head h on XCD h % 8).  XCD x
+// serves its items in that order from one counter in the caller's workspace
+// (zeroed by prefill_stream_reset_kernel before the launch), so a workgroup
+// that finishes early takes the next heaviest item; per-tile costs vary with
+// how much K/V the XCD's L2 shares, and a static deal of the same items left
+// 26 us of idle tail on C4.  Each workgroup knows its current item and the
+// next one: the next is taken (one atomic) while the current one's Q loads
+// are in flight and published to all waves before its first period.  The
+// producer may only enter items already published; when an item is so short
+// that the stream reaches the end of the published ones, the producer holds
+// on the last tile and the stream restarts (the kernel's prologue) at the
+// item it could not enter.
+// ---------------------------------------------------------------------------
+
+constexpr int kStreamMaxRanked = 2048;     // ranked query tiles (all sequences)
+constexpr int kStreamRing = 4;             // item slots: previous, current, next
+constexpr size_t kStreamWorkspaceBytes = 256;   // one work counter per XCD
+constexpr int kStreamNone = 0x7fffffff;
+
+struct StreamScratch {
+  int keys[kMaxRanked];
+  int tiles[kMaxRanked];
+  int ctx[kMaxRanked];
+  int row0[kMaxRanked];
+  int rows[kMaxRanked];
+  int2 tab[kStreamMaxRanked];     // ranked tile r: {b | qt << 8, key tiles}
+  int4 ring[kStreamRing];         // item j in slot j % 4: {b, h, qt, key tiles}; b < 0: none
+};
+
+// Key tiles walked by query tile qt of a sequence (rows S_b, context ctx_b):
+// the causal range of its last row, capped at the table's capacity.
+__device__ inline int stream_tile_keys(int S_b, int ctx_b, int qt, int cap) {
+  constexpr int kBM = kPipeWaves * kRowsPerWave;
+  const int last_row = min(qt * kBM + kBM, S_b) - 1;
+  const int kend = min(cap, ctx_b - S_b + last_row + 1);
+  return kend > 0 ? (kend + kBN - 1) / kBN : 0;
+}
+
+// Ranks the batch and fills the table of ranked tiles; returns the number of
+// items of this XCD's queue (ranked tiles x heads on the XCD).
+__device__ inline int stream_rank(const PrefillArgs& a, StreamScratch& s) {
+  constexpr int kBM = kPipeWaves * kRowsPerWave;
+  const int tid = threadIdx.x;
+  const int cap = a.MB * 16;
+  if (tid < a.B) {
+    const int rows = seq_rows(a, tid);
+    const int ctx = a.ctx[tid];
+    s.keys[tid] = rows > 0 ? min(cap, ctx) : -1;
+    s.tiles[tid] = (rows + kBM - 1) / kBM;
+    s.ctx[tid] = ctx;
+    s.row0[tid] = a.cu_q ? a.cu_q[tid] : tid * a.S;
+    s.rows[tid] = rows;
+  }
+  __syncthreads();
+  if (tid < a.B) {
+    const int k = s.keys[tid];
+    int start = 0;
+    for (int q = 0; q < a.B; ++q) {
+      const int kq = s.keys[q];
+      start += ((kq > k) | ((kq == k) & (q < tid))) ? s.tiles[q] : 0;
+    }
+    const int n = s.tiles[tid];
+    for (int t = 0; t < n && start + t < kStreamMaxRanked; ++t) {
+      const int qt = n - 1 - t;
+      s.tab[start + t] = make_int2(tid | (qt << 8),
+                                   stream_tile_keys(s.rows[tid], s.ctx[tid], qt, cap));
+    }
+  }
+  int R = 0;
+  for (int q = 0; q < a.B; ++q) R += s.tiles[q];
+  __syncthreads();
+  return min(R, kStreamMaxRanked) * (a.H / kXcds);   // the host bounds R by the same limit
+}
+
+// Item k of this XCD's queue: {b, h, qt, key tiles}, or none.
+__device__ inline int4 stream_item(const PrefillArgs& a, const StreamScratch& s, int k, int K) {
+  if (k >= K) return make_int4(-1, 0, 0, 0);
+  const int nh = a.H / kXcds;
+  const int2 e = s.tab[k / nh];
+  return make_int4(e.x & 0xff, (int)(blockIdx.x % kXcds) + kXcds * (k % nh), e.x >> 8, e.y);
+}
+
+// The producer's position in the tile stream (wave-uniform, the same in every
+// wave): key tile `kt` of the workgroup's item `it`.  Items below `allowed`
+// are published; the stream enters no other.  Where it cannot go on it holds
+// on its tile (the loads that run ahead then read that tile again) and, when
+// the reason was an unpublished item, records it in `stall_at`.
+struct StreamCursor {
+  int it, kt, nkt, row, head;
+  int allowed, stall_at;
+
+  template <int kHeadBytes>
+  __device__ inline void enter(const PrefillArgs& a, int j, const int4& e) {
+    it = j;
+    kt = 0;
+    nkt = e.w;
+    row = e.x * a.MB;
+    head = e.y / (a.H / a.Hkv) * kHeadBytes;
+  }
+  // first published item >= j that walks keys; false when there is none yet
+  template <int kHeadBytes>
+  __device__ inline bool seek(const PrefillArgs& a, const StreamScratch& s, int j) {
+    for (int nx = j;; ++nx) {
+      if (nx >= allowed) {
+        stall_at = min(stall_at, nx);
+        return false;
+      }
+      const int4 e = s.ring[nx % kStreamRing];
+      const int b = __builtin_amdgcn_readfirstlane(e.x);
+      if (b < 0) return false;
+      const int n = __builtin_amdgcn_readfirstlane(e.w);
+      if (n > 0) {
+        enter<kHeadBytes>(a, nx, make_int4(b, __builtin_amdgcn_readfirstlane(e.y), 0, n));
+        return true;
+      }
+    }
+  }
+  template <int kHeadBytes>
+  __device__ inline void advance(const PrefillArgs& a, const StreamScratch& s) {
+    if (kt + 1 < nkt) {
+      ++kt;
+      return;
+    }
+    if (stall_at != kStreamNone) return;
+    seek<kHeadBytes>(a, s, it + 1);   // on failure the cursor is unchanged
+  }
+};
+
+// PipeProducer's moves with the head of each tile taken from the stream: the
+// head's byte offset goes into the page base (the buffer resource then covers
+// the rest of the page), the lanes' offsets stay those of head 0.
+template <typename T, int D>
+struct StreamProducer {
+  static constexpr int kVD = D / 64;
+  static constexpr int kKC = D / 8;
+  static constexpr int kKU = kKC / 8;
+  static constexpr int kKeysPerKU = 64 / kKC;
+
+  uint32_t v[8];
+  uint4 k[kKU];
+  int ids;            // lanes 0..3 (mod 4): block ids of the 4 pages of one tile
+  int ids_head;       // head bytes of the tile whose ids are in `ids`
+  const char* kpage;  // K page + head of the tile whose V load_v issued
+  int k_head;
+  float chk;
+
+  int64_t page_bytes;
+  uint32_t v_off, k_off, tok_bytes;
+  int wave, lane;
+
+  __device__ inline void init(const PrefillArgs& a, int wave_) {
+    wave = wave_;
+    lane = threadIdx.x & 63;
+    chk = 0.0f;
+    tok_bytes = (uint32_t)(a.Hkv * D * (int)sizeof(T));
+    page_bytes = (int64_t)tok_bytes * 16;
+    const uint32_t tok0 = (uint32_t)(8 * (wave & 1));
+    v_off = tok0 * tok_bytes + (uint32_t)(kVD * lane * (int)sizeof(T));
+    k_off = (tok0 + (uint32_t)(lane / kKC)) * tok_bytes +
+            (uint32_t)(8 * (lane % kKC) * (int)sizeof(T));
+  }
+
+  __device__ inline void fetch_ids(const PrefillArgs& a, const StreamCursor& c) {
+    ids = a.bt[(int64_t)c.row + min(c.kt * 4 + (lane & 3), a.MB - 1)];
+    ids_head = c.head;
+  }
+
+  __device__ inline const char* page(const PrefillArgs& a, const void* base) const {
+    const int id = __builtin_amdgcn_readlane(ids, wave >> 1);
+    return reinterpret_cast<const char*>(base) + safe_block(id, a.NB) * page_bytes + ids_head;
+  }
+
+  __device__ inline __amdgpu_buffer_rsrc_t rsrc(const char* p, int head) const {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(p), (short)0,
+                                             (int)(page_bytes - head), kBufferRsrcWord3);
+  }
+
+  __device__ inline void load_v(const PrefillArgs& a) {
+    kpage = page(a, a.k);
+    k_head = ids_head;
+    const __amdgpu_buffer_rsrc_t r = rsrc(page(a, a.v), ids_head);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      if constexpr (kVD == 2) {
+        v[u] = __builtin_amdgcn_raw_buffer_load_b32(r, (int)v_off, (int)(u * tok_bytes), 0);
+      } else {
+        v[u] = __builtin_amdgcn_raw_buffer_load_b16(r, (int)v_off, (int)(u * tok_bytes), 0);
+      }
+    }
+  }
+
+  __device__ inline void load_k() {
+    const __amdgpu_buffer_rsrc_t r = rsrc(kpage, k_head);
+#pragma unroll
+    for (int u = 0; u < kKU; ++u) {
+      typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+      const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(
+          r, (int)k_off, (int)(u * kKeysPerKU * tok_bytes), 0);
+      k[u] = make_uint4(x[0], x[1], x[2], x[3]);
+    }
+  }
+
+  __device__ inline uint32_t vpair(int u, int e) const {
+    if constexpr (std::is_same_v<T, Bf16>) {
+      const float x0 = __uint_as_float(e ? (v[u] & 0xffff0000u) : (v[u] << 16));
+      const float x1 = __uint_as_float(e ? (v[u + 1] & 0xffff0000u) : (v[u + 1] << 16));
+      return pack_f16(x0, x1);
+    } else {
+      return e ? __builtin_amdgcn_perm(v[u + 1], v[u], 0x07060302u)
+               : __builtin_amdgcn_perm(v[u + 1], v[u], 0x05040100u);
+    }
+  }
+
+  __device__ inline void store_v(PipeTile<D>& t) const {
+#pragma unroll
+    for (int e = 0; e < kVD; ++e) {
+      const int d = kVD * lane + e;
+      const uint4 w = make_uint4(vpair(0, e), vpair(2, e), vpair(4, e), vpair(6, e));
+      *reinterpret_cast<uint4*>(&t.vt[d][8 * (wave ^ vt_swz<D>(d))]) = w;
+    }
+  }
+
+  __device__ inline void store_k(PipeTile<D>& t) {
+#pragma unroll
+    for (int u = 0; u < kKU; ++u) {
+      const int key = 8 * wave + kKeysPerKU * u + lane / kKC;
+      const int row = (key & ~31) | swap_bits23(key & 31);
+      const uint4 h = to_f16x8<T>(k[u]);
+      if constexpr (std::is_same_v<T, Bf16>) {
+        chk = f16_check(h, chk);
+        asm volatile("" : "+v"(chk));
+      }
+      *reinterpret_cast<uint4*>(&t.k[row][8 * (lane % kKC)]) = h;
+    }
+  }
+};
+
+// This lane's index, computed where it is used: the compiler cannot hoist
+// it, so values derived from it for one query tile are not kept in registers
+// across the whole item loop.
+__device__ inline int opaque_lane() {
+  int l;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  return l;
+}
+
+__global__ void prefill_stream_reset_kernel(int* counters) {
+  if (threadIdx.x < kXcds) counters[threadIdx.x] = 0;
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(kPipeWaves * 64) __attribute__((amdgpu_waves_per_eu(2)))
+void prefill_stream_kernel(PrefillArgs a) {
+  constexpr int kBM = kPipeWaves * kRowsPerWave;
+  constexpr int kDC16 = D / 16;
+  constexpr int kDB = D / 32;
+  constexpr int kHeadBytes = D * (int)sizeof(T);
+  using Prod = StreamProducer<T, D>;
+  __shared__ PipeTile<D> lds[kPipeBufs];
+  __shared__ StreamScratch ss;
+  __shared__ int fail[3];   // per item, rotating: some fp16 operand was inf or NaN
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int j = lane & 31;
+  const int hh = lane >> 5;
+  const int cap = a.MB * 16;
+  int* counter = a.counters + blockIdx.x % kXcds;
+  if (tid < 3) fail[tid] = 0;   // ordered by the barriers below
+
+  const int K = stream_rank(a, ss);
+  if (tid == 0) ss.ring[0] = stream_item(a, ss, atomicAdd(counter, 1), K);
+  __syncthreads();
+  if (__builtin_amdgcn_readfirstlane(ss.ring[0].x) < 0) return;
+
+  Prod pr;
+  pr.init(a, wave);
+  StreamCursor cur;
+  cur.allowed = 1;
+  cur.stall_at = kStreamNone;
+  // The stream from item j on, at stream position g: tiles g and g + 1 into
+  // their buffers, tile g + 2 in flight, the ids of tile g + 3 fetched.
+  auto prologue = [&](int jj, int g) __attribute__((always_inline)) {
+    cur.stall_at = kStreamNone;
+    if (cur.seek<kHeadBytes>(a, ss, jj)) {
+      Prod pr1 = pr;
+      pr1.chk = 0.0f;
+      pr.fetch_ids(a, cur);
+      cur.advance<kHeadBytes>(a, ss);
+      pr1.fetch_ids(a, cur);
+      cur.advance<kHeadBytes>(a, ss);
+      pr.load_v(a);
+      pr.load_k();
+      pr1.load_v(a);
+      pr1.load_k();
+      pr.fetch_ids(a, cur);
+      cur.advance<kHeadBytes>(a, ss);
+      pr.store_v(lds[g % kPipeBufs]);
+      pr.store_k(lds[g % kPipeBufs]);
+      pr1.store_v(lds[(g + 1) % kPipeBufs]);
+      pr1.store_k(lds[(g + 1) % kPipeBufs]);
+      pr.chk += pr1.chk;
+      pr.load_v(a);
+      pr.fetch_ids(a, cur);
+      cur.advance<kHeadBytes>(a, ss);
+      pr.load_k();
+    }
+    __syncthreads();
+  };
+
+  float4 qx[2 * kDC16];   // this item's fp32 Q rows in flight
+
+  // Q rows of item e: this lane's row, or the tile's last row past its end
+  auto load_q = [&](const int4& e) __attribute__((always_inline)) {
+    const int ln = opaque_lane();
+    const int S_b = __builtin_amdgcn_readfirstlane(ss.rows[e.x]);
+    const int row0 = __builtin_amdgcn_readfirstlane(ss.row0[e.x]);
+    const int i_row = e.z * kBM + wave * kRowsPerWave + (ln & 31);
+    const float* qp = a.q + ((int64_t)(row0 + min(i_row, S_b - 1)) * a.H + e.y) * D + 8 * (ln >> 5);
+#pragma unroll
+    for (int c = 0; c < kDC16; ++c) {
+      qx[2 * c] = *reinterpret_cast<const float4*>(qp + 16 * c);
+      qx[2 * c + 1] = *reinterpret_cast<const float4*>(qp + 16 * c + 4);
+    }
+  };
+
+  prologue(0, 0);
+
+  // Each iteration: the atomic that takes the next item and this item's Q
+  // loads, the next item published, this item, its output stores.
+  // (Variants that kept the Q rows or the output rows live around the loop's
+  // back edge, to overlap the Q round trip with the stores, made the
+  // allocator spill heavily.)
+  int g = 0;   // stream position of the next tile to consume
+  int slow_from = -1;
+  for (int jj = 0;; ++jj) {
+    const int4 item = ss.ring[jj % kStreamRing];
+    const int b = __builtin_amdgcn_readfirstlane(item.x);
+    const int h = __builtin_amdgcn_readfirstlane(item.y);
+    const int qt = __builtin_amdgcn_readfirstlane(item.z);
+    if (b < 0) break;
+    load_q(make_int4(b, h, qt, 0));
+    const int n_kt = __builtin_amdgcn_readfirstlane(item.w);
+    const int row0 = __builtin_amdgcn_readfirstlane(ss.row0[b]);
+    const int S_b = __builtin_amdgcn_readfirstlane(ss.rows[b]);
+    const int ctx_b = __builtin_amdgcn_readfirstlane(ss.ctx[b]);
+    const int base_pos = ctx_b - S_b;
+    const int w_first = qt * kBM + wave * kRowsPerWave;
+    const int ln = opaque_lane();
+    const int i_row = w_first + (ln & 31);
+    const bool row_ok = i_row < S_b;
+
+    // Q^T fragments
+    half8 qf[kDC16];
+    float16x o[kDB];
+    float l;
+    float qchk = 0.0f;
+    {
+      const float sc = row_ok ? a.qscale : 0.0f;
+#pragma unroll
+      for (int c = 0; c < kDC16; ++c) {
+        const float4 x0 = qx[2 * c], x1 = qx[2 * c + 1];
+        const uint4 w = make_uint4(pack_f16(x0.x * sc, x0.y * sc), pack_f16(x0.z * sc, x0.w * sc),
+                                   pack_f16(x1.x * sc, x1.y * sc), pack_f16(x1.z * sc, x1.w * sc));
+        qchk = f16_check(w, qchk);
+        qf[c] = __builtin_bit_cast(half8, w);
+      }
+    }
+    if (jj == cur.stall_at) prologue(jj, g);   // the stream broke before this item
+
+    const int lim = (row_ok ? min(base_pos + i_row, cap - 1) : -1) - 8 * (ln >> 5);
+    const int w_lim_min = min(base_pos + w_first, cap - 1);
+    const int w_lim_max = w_first < S_b ? min(base_pos + min(w_first + kRowsPerWave, S_b) - 1,
+                                              cap - 1)
+                                        : -1;
+    const int nb_w = w_lim_max < 0 ? 0 : min(2 * n_kt, w_lim_max / 32 + 1);
+    const int mask_x = w_lim_min - 31;
+    const int mask_from = mask_x < 0 ? 0 : mask_x / 32 + 1;
+    const int t_w = (nb_w + 1) / 2;
+    // The period that takes the next item from the queue: the latest one
+    // whose publication (the period after) still lets the stream enter the
+    // next item without a stop (it needs it at the end of period n_kt - 5),
+    // ~7 key tiles before this item ends.  The queue so hands out items
+    // close to the time a workgroup needs one, as a longest-first deal would.
+    const int fetch_t = max(0, n_kt - 7);
+    int next_k;   // thread 0 only
+
+    float16x bias;
+    float16x s_cur, s_nxt;
+    half8 kf[kDC16];
+    half8 vf[2][kDB];
+    half8 p[2];
+    float m;
+    auto read_k = [&](const PipeTile<D>& t, int kb) __attribute__((always_inline)) {
+  #pragma unroll
+      for (int c = 0; c < kDC16; ++c)
+        kf[c] = *reinterpret_cast<const half8*>(&t.k[kb * 32 + j][16 * c + 8 * hh]);
+    };
+    // lim is the row's last key minus 8 hh (the lane half's key offset), so
+    // that one register carries both
+    auto mask = [&](float16x& s, int blk) __attribute__((always_inline)) {
+      const int key0 = 32 * blk;
+  #pragma unroll
+      for (int r = 0; r < 16; ++r)
+        if (key0 + 16 * (r >> 3) + (r & 7) > lim) s[r] = -INFINITY;
+    };
+    const int vsw = hh ^ vt_swz<D>(j);
+    auto read_v1 = [&](const PipeTile<D>& t, int kb, int i) __attribute__((always_inline)) {
+      vf[i / kDB][i % kDB] = *reinterpret_cast<const half8*>(
+          &t.vt[32 * (i % kDB) + j][8 * ((4 * kb + 2 * (i / kDB)) ^ vsw)]);
+    };
+    auto prob2 = [&](const float16x& s, int i, uint32_t* w, float lb) __attribute__((always_inline)) {
+      w[i] = pack_f16(fast_exp2(s[2 * i]), fast_exp2(s[2 * i + 1]));
+      return __builtin_amdgcn_fdot2(__builtin_bit_cast(half2x, w[i]),
+                                    (half2x){(_Float16)1.0f, (_Float16)1.0f}, lb, false);
+    };
+    auto probs = [&](const float16x& s) __attribute__((always_inline)) {
+      uint32_t w[8];
+      float lb = 0.0f;
+  #pragma unroll
+      for (int i = 0; i < 8; ++i) lb = prob2(s, i, w, lb);
+      p[0] = __builtin_bit_cast(half8, make_uint4(w[0], w[1], w[2], w[3]));
+      p[1] = __builtin_bit_cast(half8, make_uint4(w[4], w[5], w[6], w[7]));
+      return lb;
+    };
+    auto phase_qs = [&](auto qk_tag, float16x& s_out, const float16x& sm, const PipeTile<D>& tv,
+                        int vkb) __attribute__((always_inline)) {
+      constexpr bool kQk = decltype(qk_tag)::value;
+      uint32_t w[8];
+      float lb = 0.0f;
+  #pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        if constexpr (kQk) {
+          if (i < kDC16)
+            s_out = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[i], qf[i], i == 0 ? bias : s_out, 0,
+                                                           0, 0);
+        }
+        if (i < 2 * kDB) read_v1(tv, vkb, i);
+        lb = prob2(sm, i, w, lb);
+      }
+      p[0] = __builtin_bit_cast(half8, make_uint4(w[0], w[1], w[2], w[3]));
+      p[1] = __builtin_bit_cast(half8, make_uint4(w[4], w[5], w[6], w[7]));
+      if constexpr (kQk) {
+  #pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+        }
+      }
+      return lb;
+    };
+    auto settle = [&](float lb, float16x& s, float16x& nxt, bool has_nxt) __attribute__((always_inline)) {
+      if (__builtin_amdgcn_ballot_w64(!(lb <= kPMax)) != 0) {
+        float mx = s[0];
+  #pragma unroll
+        for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[r]);
+        mx = max_halves(mx);
+        const float dlt = mx > 0.0f ? mx : 0.0f;
+        const float corr = fast_exp2(-dlt);
+        m += dlt;
+        l *= corr;
+  #pragma unroll
+        for (int d = 0; d < kDB; ++d)
+  #pragma unroll
+          for (int r = 0; r < 16; ++r) o[d][r] *= corr;
+  #pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          bias[r] -= dlt;
+          s[r] -= dlt;
+        }
+        if (has_nxt) {
+  #pragma unroll
+          for (int r = 0; r < 16; ++r) nxt[r] -= dlt;
+        }
+        lb = probs(s);
+      }
+      l += lb;
+    };
+    auto phase_pv = [&](auto read_tag, const PipeTile<D>& tk, int kkb, auto&& prod) __attribute__((always_inline)) {
+      constexpr bool kRead = decltype(read_tag)::value;
+  #pragma unroll
+      for (int i = 0; i < 2 * kDB; ++i) {
+        o[i % kDB] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[i / kDB][i % kDB], p[i / kDB],
+                                                            o[i % kDB], 0, 0, 0);
+        if constexpr (kRead) {
+          if (i < kDC16)
+            kf[i] = *reinterpret_cast<const half8*>(&tk.k[kkb * 32 + j][16 * i + 8 * hh]);
+        }
+      }
+      prod();
+      if constexpr (kRead) {
+  #pragma unroll
+        for (int i = 0; i < 2 * kDB; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
+          __builtin_amdgcn_sched_group_barrier(0x002, 3, 1);
+        }
+      }
+    };
+    using Yes = std::true_type;
+    using No = std::false_type;
+    // the producer's share of a period: V of the tile two ahead into LDS, the
+    // next tile's V loads, the ids of the tile after it; then K likewise
+    // The next item is taken from the queue in period fetch_t (thread 0's
+    // atomic, just before the period's V loads) and published in the next
+    // period, after store_v has waited for those loads and with them for the
+    // atomic.
+    auto prod_v = [&](PipeTile<D>& tw, int t) __attribute__((always_inline)) {
+      return [&pr, &tw, &a, &cur, &next_k, counter, K, t, fetch_t, jj, tid]() {
+        pr.store_v(tw);
+        if (t == fetch_t + 1 && tid == 0)
+          ss.ring[(jj + 1) % kStreamRing] = stream_item(a, ss, next_k, K);
+        if (t == fetch_t && tid == 0) next_k = atomicAdd(counter, 1);
+        pr.load_v(a);
+        pr.fetch_ids(a, cur);
+      };
+    };
+    auto prod_k = [&](PipeTile<D>& tw) __attribute__((always_inline)) {
+      return [&pr, &tw]() {
+        pr.store_k(tw);
+        pr.load_k();
+      };
+    };
+    // end of a period: the cursor moves to the tile whose ids the next period
+    // fetches (its LDS reads are covered by the barrier's wait)
+    auto end_period = [&](int t) __attribute__((always_inline)) {
+      cur.advance<kHeadBytes>(a, ss);
+      __syncthreads();
+      if (t == fetch_t + 1) cur.allowed = jj + 2;
+    };
+
+#pragma unroll
+    for (int d = 0; d < kDB; ++d)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[d][r] = 0.0f;
+    m = kNegBig;
+    l = 0.0f;
+    if (t_w > 0) {
+      const PipeTile<D>& t0 = lds[g % kPipeBufs];
+      read_k(t0, 0);
+      float16x zero;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) zero[r] = 0.0f;
+      s_cur = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[0], qf[0], zero, 0, 0, 0);
+#pragma unroll
+      for (int c = 1; c < kDC16; ++c)
+        s_cur = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[c], qf[c], s_cur, 0, 0, 0);
+      if (mask_from == 0) mask(s_cur, 0);
+      float mx = s_cur[0];
+#pragma unroll
+      for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s_cur[r]);
+      m = fmaxf(kNegBig, max_halves(mx));
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        bias[r] = -m;
+        s_cur[r] -= m;
+      }
+      read_k(t0, 1);
+    }
+
+    // the item's periods: stream tile g + t consumed, g + t + 2 written,
+    // g + t + 3 loaded, ids of g + t + 4 fetched
+    int t = 0;
+    for (; t + 1 < t_w; ++t) {
+      const PipeTile<D>& tc = lds[(g + t) % kPipeBufs];
+      const PipeTile<D>& tn = lds[(g + t + 1) % kPipeBufs];
+      PipeTile<D>& tw = lds[(g + t + 2) % kPipeBufs];
+      if (2 * t >= mask_from) mask(s_cur, 2 * t);
+      float lb = phase_qs(Yes{}, s_nxt, s_cur, tc, 0);
+      settle(lb, s_cur, s_nxt, true);
+      phase_pv(Yes{}, tn, 0, prod_v(tw, t));
+      if (2 * t + 1 >= mask_from) mask(s_nxt, 2 * t + 1);
+      lb = phase_qs(Yes{}, s_cur, s_nxt, tc, 1);
+      settle(lb, s_nxt, s_cur, true);
+      phase_pv(Yes{}, tn, 1, prod_k(tw));
+      end_period(t);
+    }
+    if (t < t_w) {
+      const PipeTile<D>& tc = lds[(g + t) % kPipeBufs];
+      PipeTile<D>& tw = lds[(g + t + 2) % kPipeBufs];
+      const bool second = 2 * t + 1 < nb_w;
+      if (2 * t >= mask_from) mask(s_cur, 2 * t);
+      if (second) {
+        s_nxt = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[0], qf[0], bias, 0, 0, 0);
+#pragma unroll
+        for (int c = 1; c < kDC16; ++c)
+          s_nxt = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[c], qf[c], s_nxt, 0, 0, 0);
+      }
+      float lb = phase_qs(No{}, s_nxt, s_cur, tc, 0);
+      settle(lb, s_cur, s_nxt, second);
+      phase_pv(No{}, tc, 0, prod_v(tw, t));
+      if (second) {
+        if (2 * t + 1 >= mask_from) mask(s_nxt, 2 * t + 1);
+        lb = phase_qs(No{}, s_cur, s_nxt, tc, 1);
+        settle(lb, s_nxt, s_cur, false);
+        phase_pv(No{}, tc, 1, prod_k(tw));
+      } else {
+        prod_k(tw)();
+      }
+      end_period(t);
+      ++t;
+    }
+    for (; t < n_kt; ++t) {
+      PipeTile<D>& tw = lds[(g + t + 2) % kPipeBufs];
+      prod_v(tw, t)();
+      prod_k(tw)();
+      end_period(t);
+    }
+    g += n_kt;
+    if (fetch_t + 1 >= n_kt) {
+      // an item of at most one period: its successor is taken here (the
+      // stream will have stopped short of it and restarts there)
+      if (tid == 0) {
+        if (n_kt == 0) next_k = atomicAdd(counter, 1);
+        ss.ring[(jj + 1) % kStreamRing] = stream_item(a, ss, next_k, K);
+      }
+      __syncthreads();
+      cur.allowed = jj + 2;
+    }
+
+    // ---- range check (the rows are stored at the top of the next
+    // iteration).  The conversion check covers every tile this wave converted
+    // so far, which includes this item's; a failure therefore also sends the
+    // items after it to the fp32 path.
+    bool my_fail = f16_check_failed(pr.chk + qchk);
+    {
+      float oc = 0.0f;
+#pragma unroll
+      for (int d = 0; d < kDB; ++d)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) oc += o[d][r] * 0.0f;
+      my_fail = my_fail || !(oc == 0.0f);
+    }
+    // fail[jj % 3]: set by any wave of item jj, read after the barrier,
+    // cleared by thread 0 two items later (every read of it is then past a
+    // barrier that thread 0 has also passed)
+    if (my_fail) fail[jj % 3] = 1;
+    if (tid == 0) fail[(jj + 1) % 3] = 0;
+    __syncthreads();
+    if (fail[jj % 3] != 0) {
+      slow_from = jj;   // this item and every later one: fp32, below
+      break;
+    }
+    {   // the normalised rows
+      const float lsum = sum_halves(l);
+      const int le = opaque_lane();
+      const int i_out = w_first + (le & 31);
+      if (i_out < S_b) {
+        const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
+        float* op = a.out + ((int64_t)(row0 + i_out) * a.H + h) * D + 4 * (le >> 5);
+#pragma unroll
+        for (int d = 0; d < kDB; ++d)
+#pragma unroll
+          for (int gq = 0; gq < 4; ++gq)
+            *reinterpret_cast<float4*>(op + d * 32 + 8 * gq) =
+                make_float4(o[d][4 * gq] * inv, o[d][4 * gq + 1] * inv, o[d][4 * gq + 2] * inv,
+                            o[d][4 * gq + 3] * inv);
+      }
+    }
+  }
+  // the loads that ran ahead of the last period are not consumed; let them
+  // land before the waves end
+  __builtin_amdgcn_s_waitcnt(0);
+  if (slow_from < 0) return;
+
+  // Some fp16 operand of item slow_from was out of range.  The conversion
+  // check accumulates over all tiles a wave converted, so the matrix-core
+  // loop is left for good: this item and the workgroup's remaining ones are
+  // computed with fp32 arithmetic, one at a time (the next item is already
+  // published; each later one is taken from the queue here).
+  for (int jj = slow_from;; ++jj) {
+    const int4 item = ss.ring[jj % kStreamRing];
+    const int b = __builtin_amdgcn_readfirstlane(item.x);
+    if (b < 0) break;
+    const int h = __builtin_amdgcn_readfirstlane(item.y);
+    const int qt = __builtin_amdgcn_readfirstlane(item.z);
+    const int n_kt = __builtin_amdgcn_readfirstlane(item.w);
+    const int row0 = __builtin_amdgcn_readfirstlane(ss.row0[b]);
+    const int S_b = __builtin_amdgcn_readfirstlane(ss.rows[b]);
+    const int ctx_b = __builtin_amdgcn_readfirstlane(ss.ctx[b]);
+    prefill_rows_fp32<T, D>(a, b, h, h / (a.H / a.Hkv), row0, S_b, ctx_b - S_b, cap,
+                            qt * kBM + wave * kRowsPerWave, 0, n_kt * kBN, 0);
+    const bool more = __builtin_amdgcn_readfirstlane(ss.ring[(jj + 1) % kStreamRing].x) >= 0;
+    if (tid == 0 && more)
+      ss.ring[(jj + 2) % kStreamRing] = stream_item(a, ss, atomicAdd(counter, 1), K);
+    __syncthreads();
+  }
+}
+
 // Merge of a split prefill: for row i of sequence b and head h,
 //   out = sum_p w_p O_p / sum_p w_p l_p,  w_p = exp2(m_p - max_p m_p)
 // over the n_split parts (a part without keys for the row has m_p = -3e38 and
@@ -1327,7 +2037,7 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a) {
 // first when the batch has at most kMaxRanked sequences; a split multiplies
 // each ranked tile's slots by n_split (parts next to each other).
 template <typename T, int D, int W>
-int launch_typed(PrefillArgs a, int max_rows_per_seq, hipStream_t stream) {
+int launch_typed(PrefillArgs a, int max_rows_per_seq, int stream_ns, hipStream_t stream) {
   constexpr int kBM = Shape<D, W>::kBM;
   a.n_qt = (max_rows_per_seq + kBM - 1) / kBM;
   const int64_t pairs = (int64_t)a.B * a.H;
@@ -1340,10 +2050,17 @@ int launch_typed(PrefillArgs a, int max_rows_per_seq, hipStream_t stream) {
   const dim3 grid((unsigned)(kXcds * a.slots_per_xcd)), block(Shape<D, W>::kThreads);
   // 8-wave workgroups at head dim 64 and 128 take the pipelined kernel; the
   // 4-wave shape (small grids without a workspace, head dim 32) the other
-  if constexpr (W == kPipeWaves && D >= 64)
-    hipLaunchKernelGGL((prefill_pipe_kernel<T, D>), grid, block, 0, stream, a);
-  else
+  if constexpr (W == kPipeWaves && D >= 64) {
+    if (stream_ns > 0) {
+      hipLaunchKernelGGL(prefill_stream_reset_kernel, dim3(1), dim3(64), 0, stream, a.counters);
+      hipLaunchKernelGGL((prefill_stream_kernel<T, D>), dim3((unsigned)(kXcds * stream_ns)), block,
+                         0, stream, a);
+    } else {
+      hipLaunchKernelGGL((prefill_pipe_kernel<T, D>), grid, block, 0, stream, a);
+    }
+  } else {
     hipLaunchKernelGGL((prefill_mfma_kernel<T, D, W>), grid, block, 0, stream, a);
+  }
   if (a.n_split > 1) {
     // the workspace of B * rows_cap * H * (D + 2) floats per part exists, so
     // this product fits; the grid must still fit one launch
@@ -1355,15 +2072,16 @@ int launch_typed(PrefillArgs a, int max_rows_per_seq, hipStream_t stream) {
 }
 
 template <typename T>
-int launch_dim(const PrefillArgs& a, int D, bool wide, int max_rows_per_seq, hipStream_t stream) {
+int launch_dim(const PrefillArgs& a, int D, bool wide, int max_rows_per_seq, int stream_ns,
+               hipStream_t stream) {
   switch (D) {
-    case 32: return launch_typed<T, 32, 4>(a, max_rows_per_seq, stream);
+    case 32: return launch_typed<T, 32, 4>(a, max_rows_per_seq, 0, stream);
     case 64:
-      return wide ? launch_typed<T, 64, 8>(a, max_rows_per_seq, stream)
-                  : launch_typed<T, 64, 4>(a, max_rows_per_seq, stream);
+      return wide ? launch_typed<T, 64, 8>(a, max_rows_per_seq, stream_ns, stream)
+                  : launch_typed<T, 64, 4>(a, max_rows_per_seq, 0, stream);
     case 128:
-      return wide ? launch_typed<T, 128, 8>(a, max_rows_per_seq, stream)
-                  : launch_typed<T, 128, 4>(a, max_rows_per_seq, stream);
+      return wide ? launch_typed<T, 128, 8>(a, max_rows_per_seq, stream_ns, stream)
+                  : launch_typed<T, 128, 4>(a, max_rows_per_seq, 0, stream);
     default: return fail(HS_EUNSUPPORTED, "unsupported head_dim for the MFMA path: " +
                                               std::to_string(D));
   }
@@ -1377,11 +2095,25 @@ int launch_dim(const PrefillArgs& a, int D, bool wide, int max_rows_per_seq, hip
 // workspace, each tile's key range is split over floor(cus / tiles) <= 4
 // workgroups (a 1024-row chunk of 32 heads: 128 tiles, 2 parts); without one,
 // 128-row workgroups, which run one wave per SIMD but reach twice as many CUs.
+//
+// With a workspace, full-width grids of at least two query tiles per CU run
+// the persistent kernel instead (stream_ns workgroups per XCD, one per CU):
+// it needs whole XCDs of heads (H % 8 == 0), the ranked dispatch and at most
+// kStreamMaxRanked ranked tiles.  HETEROSERVE_PREFILL_GRID=1 keeps the grid
+// kernel (for comparisons).
 PrefillPlan plan_prefill_mfma(int B, int max_rows, int H, int D, int cus, bool can_split) {
   const int bm = D >= 64 ? 256 : 128;
   const int64_t tiles = sat_mul(B, ceil_div(max_rows, bm), H);
-  PrefillPlan p{true, 1};
-  if (tiles >= cus) return p;
+  PrefillPlan p{true, 1, 0};
+  if (tiles >= cus) {
+    const char* env = std::getenv("HETEROSERVE_PREFILL_GRID");
+    const bool grid_only = env && env[0] == '1';
+    const int64_t ranked = sat_mul(B, ceil_div(max_rows, bm));
+    if (can_split && !grid_only && D >= 64 && B <= kMaxRanked && H % kXcds == 0 &&
+        ranked <= kStreamMaxRanked && tiles >= 2 * (int64_t)cus && cus >= kXcds)
+      p.stream_ns = cus / kXcds;
+    return p;
+  }
   const int64_t splits = std::min<int64_t>(kMaxSplit, tiles > 0 ? cus / tiles : 1);
   if (can_split && splits >= 2 && B <= kMaxRanked) p.n_split = (int)splits;
   else p.wide = false;
@@ -1390,6 +2122,7 @@ PrefillPlan plan_prefill_mfma(int B, int max_rows, int H, int D, int cus, bool c
 
 // INT64_MAX when the sizes do not fit
 int64_t prefill_workspace_bytes(const PrefillPlan& p, int B, int max_rows, int H, int D) {
+  if (p.stream_ns > 0) return (int64_t)kStreamWorkspaceBytes;
   if (p.n_split < 2) return 0;
   const int64_t pairs = sat_mul(p.n_split, B, max_rows, H);
   const int64_t o_bytes = sat_add(sat_mul(pairs, D, (int64_t)sizeof(float)), 255) / 256 * 256;
@@ -1421,9 +2154,16 @@ int launch_prefill_mfma(const float* q, const int32_t* cu_q, int S, int max_rows
   if (hipGetDevice(&dev) != hipSuccess) return fail(HS_EHIP, "hipGetDevice failed");
   const int cus = hs_device_cu_count(dev);
   if (cus <= 0) return fail(HS_EHIP, "could not read the device CU count");
-  const PrefillPlan plan = plan_prefill_mfma(B, max_rows_per_seq, H, D, cus, workspace != nullptr);
+  PrefillPlan plan = plan_prefill_mfma(B, max_rows_per_seq, H, D, cus, workspace != nullptr);
   a.n_split = plan.n_split;
   a.rows_cap = max_rows_per_seq;
+  if (plan.stream_ns > 0) {
+    if (workspace_bytes < kStreamWorkspaceBytes)
+      return fail(HS_EWORKSPACE, "prefill workspace too small: " +
+                                     std::to_string(kStreamWorkspaceBytes) + " bytes needed");
+    if (sat_mul(B, MB) > 0x7fffffffLL) plan.stream_ns = 0;   // table rows as int: grid kernel
+    a.counters = static_cast<int*>(workspace);
+  }
   if (plan.n_split > 1) {
     const int64_t need_i = prefill_workspace_bytes(plan, B, max_rows_per_seq, H, D);
     if (need_i == INT64_MAX) return fail(HS_EUNSUPPORTED, "prefill split too large");
@@ -1437,8 +2177,10 @@ int launch_prefill_mfma(const float* q, const int32_t* cu_q, int S, int max_rows
   }
   profile_begin(stream);
   int rc;
-  if (kv_dtype == HS_DTYPE_F16) rc = launch_dim<_Float16>(a, D, plan.wide, max_rows_per_seq, stream);
-  else rc = launch_dim<Bf16>(a, D, plan.wide, max_rows_per_seq, stream);
+  if (kv_dtype == HS_DTYPE_F16)
+    rc = launch_dim<_Float16>(a, D, plan.wide, max_rows_per_seq, plan.stream_ns, stream);
+  else
+    rc = launch_dim<Bf16>(a, D, plan.wide, max_rows_per_seq, plan.stream_ns, stream);
   profile_end(stream);
   if (rc != HS_OK) return rc;
   return check_launch("MFMA prefill");

@@ -9,6 +9,9 @@ point called while the library is unavailable raises RuntimeError.
 Environment:
   HETEROSERVE_DISABLE_CUDA_KERNEL  treat the library as unavailable (reference flag)
   HETEROSERVE_HIP_LIB              path of libhsattn.so (default: next to this file)
+  HETEROSERVE_PREFILL_GRID=1       keep the MFMA prefill on its grid kernel (one workgroup
+                                   per query tile) where the persistent one would run;
+                                   read at each call, for comparisons
 
 PyTorch provides device memory and the current stream; every kernel launches
 on ``torch.cuda.current_stream(device)`` of the input's device.

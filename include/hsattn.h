@@ -209,9 +209,12 @@ int hs_decode_shared(const float* q, const void* k_cache, const void* v_cache, i
  * device; 0 when they need none.  Only the matrix-core path (use_mfma = 1)
  * uses one: when its query tiles cannot cover every CU, each tile's key range
  * is split over up to 4 workgroups, whose partial results (fp32, (D + 2) * 4
- * bytes per part, row and head) are merged by a second kernel.  No reference
- * counterpart (the reference's prefill has no split); version 3 of the ABI
- * added it and the workspace arguments below.
+ * bytes per part, row and head) are merged by a second kernel; when they give
+ * every CU at least two (head dim 64 or 128, H a multiple of 8, at most 256
+ * sequences), a persistent kernel of one workgroup per CU takes them from
+ * per-XCD queues whose 256 bytes of counters are the workspace (zeroed by
+ * the call itself).  No reference counterpart (the reference's prefill has
+ * neither); version 3 of the ABI added the workspace arguments below.
  */
 size_t hs_prefill_workspace_bytes(int B, int max_seqlen_q, int H, int D, int use_mfma);
 
@@ -237,9 +240,9 @@ size_t hs_prefill_workspace_bytes(int B, int max_seqlen_q, int H, int D, int use
  *   q   [B, S, H, D] float32;  out [B, S, H, D] float32
  *   workspace  NULL, or device scratch of hs_prefill_workspace_bytes(B, S, H,
  *              D, use_mfma) bytes.  NULL runs without the key-range split
- *              (narrower workgroups instead); a workspace smaller than the
- *              split needs is HS_EWORKSPACE.  Calls that overlap in time must
- *              not share one.
+ *              (narrower workgroups instead) and without the persistent
+ *              kernel; a workspace smaller than the plan needs is
+ *              HS_EWORKSPACE.  Calls that overlap in time must not share one.
  */
 int hs_prefill(const float* q, const void* k_cache, const void* v_cache, int kv_dtype,
                int num_blocks, const int32_t* block_tables, const int32_t* context_lens,
