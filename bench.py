@@ -75,7 +75,7 @@ LEG_KERNELS = {
     "B64-4k": ("hs::row_attn_part_kernel<hs::Bf16, 128, true, 1>", 8192, "every leg"),
     "C1": ("hs::row_attn_wg_kernel<_Float16, 64, true, 1, 16>", None, "every leg"),
     "C2-gqa": ("hs::splitmm_even_kernel<hs::Bf16Ops, 128, true, 4>", None, "every leg"),
-    "C4": ("hs::prefill_pipe_kernel<hs::Bf16, 128>", 1536, "every leg"),
+    "C4": ("hs::prefill_stream_kernel<hs::Bf16, 128>", None, "every leg"),
     "C5_pack": ("hs::page_copy_kernel<false, true>", None, "every leg"),
     "C5_unpack": ("hs::page_copy_kernel<true, true>", None, "every leg"),
 }
@@ -1158,7 +1158,7 @@ def main() -> int:
             "kernel_tflops": round(pre["kernel_tflops"], 2),
             "mfma_frac": round(pre["kernel_tflops"] / MFMA_F16_PEAK_TFLOPS, 4),
             "useful_flops": pre["flops"],
-            "roofline": roofline("mfma", "prefill_pipe_kernel<Bf16, 128>", pre["flops"],
+            "roofline": roofline("mfma", "prefill_stream_kernel<Bf16, 128>", pre["flops"],
                                  pre["kernel_ms"], leg_traffic("C4")),
         }
         log(f"C4 prefill: {pre['step_ms'] * 1e3:.1f} us, {pre['kernel_tflops']:.1f} TFLOP/s")

