@@ -179,3 +179,36 @@ def test_stream_workspace_must_hold_the_queue():
     assert b"workspace" in lib.hs_last_error()
     torch.cuda.synchronize()
     assert not out.any()
+
+
+def test_stream_under_graph_capture():
+    """The persistent prefill captured in a HIP graph: its queue reset is a
+    kernel (no memset node), so each replay starts from zeroed counters.
+    Three replays, with eager work between them, equal the eager call bit for
+    bit."""
+    case = _case(**SHAPES["gqa"])
+    assert _plans_stream(case)
+    want = _run(case, grid=False)
+
+    from heteroserve import _hip
+
+    def call():
+        return _hip.prefill_varlen(case.q, case.cu_seqlens, int(case.q_lens.max()),
+                                   case.k_cache, case.v_cache, case.block_tables,
+                                   case.context_lens, case.scale, use_mfma=True)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        call()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = call()
+    for i in range(3):
+        out.fill_(float("nan"))
+        _run(case, grid=True)   # eager work between the replays
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), f"replay {i}"
