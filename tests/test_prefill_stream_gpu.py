@@ -110,6 +110,14 @@ SHAPES = {
                               222, 48, 111, 300, 7, 160, 245, 70, 19, 290, 135, 240, 56, 12,
                               201, 99, 260, 150, 38, 177, 288, 3, 120, 215, 66, 254],
                        H=32, Hkv=8, D=128, dtype=torch.bfloat16, seed=4),
+    # 64 heads (8 per XCD), 8 query heads per KV head, fp16 cache at head dim 128
+    "h64-f16": dict(prefix=[700, 2900, 0, 1500, 64, 333, 2048, 10],
+                    chunk=[900, 300, 1100, 257, 640, 1000, 128, 700],
+                    H=64, Hkv=8, D=128, dtype=torch.float16, seed=7),
+    # 200 sequences (near the 256 the ranking holds), short chunks, head dim 64
+    "many-seqs": dict(prefix=[int(x) for x in np.random.default_rng(8).integers(0, 3000, 200)],
+                      chunk=[int(x) for x in np.random.default_rng(9).integers(1, 600, 200)],
+                      H=16, Hkv=16, D=64, dtype=torch.bfloat16, seed=8),
 }
 
 
