@@ -66,20 +66,20 @@ def log(*a) -> None:
 TRAFFIC_PROFILE = ROOT / "profiles" / "bench_legs_trace_and_traffic.md"
 # Each leg's dominant kernel as rocprofv3 names it, its grid in workgroups
 # (None: the only grid that kernel ran with) and the profile's table that
-# holds it.  C2's launch (64 rows x 16 partitions of 512 tokens x 16 two-head
-# workgroups) and C3's (16 rows x 64 partitions x 16) have the same grid, so
-# the run of every leg averages them in one row: each is profiled alone.
+# holds it.  C2, C3 and B64-4k run the multi-head even split, whose grid (16
+# two-head workgroups x one range per resident workgroup) is the same for all
+# three, so the run of every leg averages them in one row: each is profiled
+# alone.
 LEG_KERNELS = {
-    "C2": ("hs::row_attn_part_kernel<hs::Bf16, 128, true, 1>", 16384, "C2 alone"),
-    "C3": ("hs::row_attn_part_kernel<hs::Bf16, 128, true, 1>", 16384, "C3 alone"),
-    "B64-4k": ("hs::row_attn_part_kernel<hs::Bf16, 128, true, 1>", 8192, "every leg"),
+    "C2": ("hs::row_attn_even_kernel<hs::Bf16, 128>", None, "C2 alone"),
+    "C3": ("hs::row_attn_even_kernel<hs::Bf16, 128>", None, "C3 alone"),
+    "B64-4k": ("hs::row_attn_even_kernel<hs::Bf16, 128>", None, "B64-4k alone"),
     "C1": ("hs::row_attn_wg_kernel<_Float16, 64, true, 1, 16>", None, "every leg"),
     "C2-gqa": ("hs::splitmm_even_kernel<hs::Bf16Ops, 128, true, 4>", None, "every leg"),
     "C4": ("hs::prefill_stream_kernel<hs::Bf16, 128>", None, "every leg"),
     "C5_pack": ("hs::page_copy_kernel<false, true>", None, "every leg"),
     "C5_unpack": ("hs::page_copy_kernel<true, true>", None, "every leg"),
 }
-DECODE_KERNEL, DECODE_WORKGROUPS, _ = LEG_KERNELS["C2"]
 
 
 def profiled_traffic(kernel: str, workgroups, table: str = "every leg"):
@@ -1014,13 +1014,14 @@ def decode_config(case, partition: int) -> dict:
         "head_dim": case.head_dim, "block_size": 16, "kv_dtype": kv_dtype,
         "sum_context": int(case.ctx.sum()), "max_context": int(case.ctx.max()),
         "num_blocks": int(case.k_cache.shape[0]),
+        # (C1, a grid too small to fill the CUs, takes the small-grid form)
         "decomposition": (f"fixed partitions of {partition} tokens + LSE merge"
                           if partition else
+                          "library default: one workgroup per (row, head), keys split over "
+                          "its waves, no merge"
+                          if case.name == "C1" else
                           "library default: even split (all pages cut into one equal range "
-                          "per resident workgroup, then an LSE merge of the rows cut)"
-                          if case.kv_heads < case.n_heads <= 4 * case.kv_heads else
-                          "library default partitions (512 tokens, halved down to 32 while "
-                          "the grid has fewer than 4 waves per CU) + LSE merge"),
+                          "per resident workgroup, then an LSE merge of the rows cut)"),
         "parallelism": "none (one GPU)",
     }
     if case.meta.get("shared_blocks"):

@@ -203,11 +203,12 @@ static int64_t decode_ws_bytes(int64_t rows, int H, int D, int P) {
 // Sizes a query function cannot report (0 means "none needed" there).
 constexpr int64_t kTooLarge = INT64_MAX;
 
-// The default decomposition of the grouped-query matrix-core decode with up
-// to 4 query heads per KV head (16-bit caches, 16-token pages), on grids
-// large enough: the even split (mode 4, hs_decode_splitmm.hip), one equal
-// share of all pages per workgroup, then a merge of the rows it cut.  Calls
-// that name a partition or a split count keep those decompositions.
+// The default decomposition of decode with up to 4 query heads per KV head
+// (16-bit caches, 16-token pages; the split-operand matrix cores for grouped
+// heads, the VALU walk for plain multi-head attention), on grids large
+// enough: the even split (mode 4, hs_decode_splitmm.hip), one equal share of
+// all pages per workgroup, then a merge of the rows it cut.  Calls that name
+// a partition or a split count keep those decompositions.
 static bool even_applies(int kv_dtype, int BS, int D, int B, int H, int Hkv, int MB,
                          int num_splits, int partition_tokens) {
   return num_splits == 0 && partition_tokens == 0 && BS == 16 &&

@@ -308,7 +308,7 @@ static int launch_dim(const RowAttnArgs& a, int D, hipStream_t stream) {
 // waited for whole CUs to drain and finished last.
 int launch_row_attn(const RowAttnArgs& a, int kv_dtype, int D, hipStream_t stream,
                     const SharePlanArgs* shared) {
-  if (a.mode == 4) {   // even split: prep + one kernel, no merge (hs_decode_splitmm.hip)
+  if (a.mode == 4) {   // even split, then the merge of the rows it cut (hs_decode_splitmm.hip)
     const int64_t gx = sat_mul(a.Hkv, ceil_div(a.H / a.Hkv, 16), a.even_m);
     if (gx > 0x7fffffffLL) return fail(HS_EUNSUPPORTED, "grid too large");
     launch_splitmm_even(a, kv_dtype, D, stream);

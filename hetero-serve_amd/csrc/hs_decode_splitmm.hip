@@ -75,6 +75,7 @@
 #include <utility>
 
 #include "hs_kernels.h"
+#include "hs_rowwalk.h"
 
 namespace hs {
 
@@ -583,36 +584,24 @@ __device__ inline int64_t range_pages(const RowAttnArgs& a, int64_t tp) {
   return max((int64_t)1, (tp + m - 1) / m);
 }
 
-template <typename Ops, int D, bool kCols, int kW>
-__global__ __launch_bounds__(64 * kW) void splitmm_even_kernel(RowAttnArgs a) {
-  __shared__ PageLds<D> lds[kW];
-  __shared__ float wave_m[kW][kSlots], wave_l[kW][kSlots];
+// Range wr of the even split: pages [s, e) of the rows laid end to end,
+// and its first row r with R_r, the pages of the rows before it (R_r <= s <
+// R_{r+1}).  Every lane computes the same (scalar) values; false for an
+// empty range.  (The first 64 rows' pages stay in registers between the two
+// passes.)
+__device__ inline bool even_range(const RowAttnArgs& a, int wr, int64_t& s, int64_t& e, int& r,
+                                  int64_t& Rr) {
   const int lane = threadIdx.x & 63;
-  const int wv = threadIdx.x >> 6;
-  const int G = a.H / a.Hkv;
-  const int n_hc = (G + kSlots - 1) / kSlots;
-  const int n_units = a.Hkv * n_hc;
-  const int kg = min(G, kSlots);                        // state rows per slot
-  const int unit = (int)(blockIdx.x % n_units);         // unit-fastest: units spread over XCDs
-  const int wr = (int)(blockIdx.x / n_units);           // this workgroup's range, < M
-  const int kvh = unit / n_hc;
-  const int hc = unit - kvh * n_hc;
-  const int h0 = kvh * G + hc * kSlots;
-  const int gc = min(kSlots, G - hc * kSlots);
-
-  // This range [s, e) and its first row r (R_r <= s < R_{r+1}); every wave
-  // computes the same (scalar) values.
-  // (The first 64 rows' pages stay in registers between the two passes.)
   const int64_t v0 = lane < a.B ? row_pages(a, lane) : 0;
   int64_t tp = wave_sum64(v0);
   for (int c = 64; c < a.B; c += 64)
     tp += wave_sum64(c + lane < a.B ? row_pages(a, c + lane) : 0);
   const int64_t Q = range_pages(a, tp);
-  const int64_t s = (int64_t)wr * Q;
-  const int64_t e = min(s + Q, tp);
-  if (s >= e) return;                                   // workgroup-uniform
-  int r = a.B;
-  int64_t Rr = tp;
+  s = (int64_t)wr * Q;
+  e = min(s + Q, tp);
+  if (s >= e) return false;
+  r = a.B;
+  Rr = tp;
   int64_t base = 0;
   for (int c = 0; c < a.B; c += 64) {
     const int64_t v = c == 0 ? v0 : (c + lane < a.B ? row_pages(a, c + lane) : 0);
@@ -631,6 +620,29 @@ __global__ __launch_bounds__(64 * kW) void splitmm_even_kernel(RowAttnArgs a) {
     }
     base += lane_value64(inc, 63);
   }
+  return true;
+}
+
+template <typename Ops, int D, bool kCols, int kW>
+__global__ __launch_bounds__(64 * kW) void splitmm_even_kernel(RowAttnArgs a) {
+  __shared__ PageLds<D> lds[kW];
+  __shared__ float wave_m[kW][kSlots], wave_l[kW][kSlots];
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  const int G = a.H / a.Hkv;
+  const int n_hc = (G + kSlots - 1) / kSlots;
+  const int n_units = a.Hkv * n_hc;
+  const int kg = min(G, kSlots);                        // state rows per slot
+  const int unit = (int)(blockIdx.x % n_units);         // unit-fastest: units spread over XCDs
+  const int wr = (int)(blockIdx.x / n_units);           // this workgroup's range, < M
+  const int kvh = unit / n_hc;
+  const int hc = unit - kvh * n_hc;
+  const int h0 = kvh * G + hc * kSlots;
+  const int gc = min(kSlots, G - hc * kSlots);
+
+  int64_t s, e, Rr;
+  int r;
+  if (!even_range(a, wr, s, e, r, Rr)) return;          // workgroup-uniform
 
   float4x o[D / 16];
   float m, l;
@@ -650,6 +662,53 @@ __global__ __launch_bounds__(64 * kW) void splitmm_even_kernel(RowAttnArgs a) {
       write_unit_state<D, kCols, kW>(o, m, l, gc, pa == Rr && pb == Rn, a.out + orow0,
                                      a.part_acc + slot * D, D, a.part_ml + 2 * slot, 1, lds,
                                      wave_m, wave_l);
+    }
+    Rr = Rn;
+  }
+}
+
+// The even split for plain multi-head attention (one query head per KV head)
+// on the VALU walk: a workgroup is kEvenValuWaves adjacent heads (each its
+// own unit: the merge's slot layout with one state row per slot) and one
+// range wr; each wave walks its head's pieces of the range with RowWalk
+// (hs_rowwalk.h), the fixed-partition kernel's arithmetic, and writes a whole
+// row's output or a cut row's state.  Adjacent heads read adjacent 256-byte
+// pieces of each token row, as in the partition kernel.
+constexpr int kEvenValuWaves = 2;
+
+template <typename T, int D>
+__global__ __launch_bounds__(64 * kEvenValuWaves)
+__attribute__((amdgpu_waves_per_eu(D > 128 ? 3 : 4))) void row_attn_even_kernel(RowAttnArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int n_hp = (a.H + kEvenValuWaves - 1) / kEvenValuWaves;
+  const int hp = (int)(blockIdx.x % n_hp);              // head pairs fastest: token rows together
+  const int wr = (int)(blockIdx.x / n_hp);
+  const int h = hp * kEvenValuWaves + (int)(threadIdx.x >> 6);
+  if (h >= a.H) return;                                 // the waves share nothing
+  int64_t s, e, Rr;
+  int r;
+  if (!even_range(a, wr, s, e, r, Rr)) return;
+  const int64_t cap = (int64_t)a.MB * a.BS;
+  for (; r < a.B && Rr < e; ++r) {                      // wave-uniform
+    const int pr = row_pages(a, r);
+    const int64_t Rn = Rr + pr;
+    if (pr > 0) {
+      const int64_t pa = max(s, Rr), pb = min(e, Rn);   // pa < pb: this row's piece
+      const int end = (int)min((int64_t)a.ctx[r], cap);
+      const int lo = (int)(pa - Rr) * kPage;
+      const int hi = (int)min((pb - Rr) * kPage, (int64_t)end);
+      const int64_t orow = ((int64_t)r * a.H + h) * D;
+      RowWalk<T, D, true, 1> w;
+      w.run(KvPages{a.k, a.v, a.Hkv, a.BS, a.NB}, a.q + orow, a.qscale, h, a.bt + (int64_t)r * a.MB,
+            lo, hi);
+      if (w.slot(lane) == 0) {
+        if (pa == Rr && pb == Rn) {
+          w.store_out(0, a.out + orow);
+        } else {
+          const int64_t slot = (int64_t)h * a.even_slots + wr + r;
+          w.store_state(0, a.part_acc + slot * D, reinterpret_cast<float2*>(a.part_ml) + slot);
+        }
+      }
     }
     Rr = Rn;
   }
@@ -847,6 +906,28 @@ static const void* even_kernel(int kv_dtype, int D) {
 
 int splitmm_even_min_pages() { return kEvenMinPages; }
 
+// Plain multi-head attention (H == Hkv) on 16-bit caches with 16-token
+// pages: the VALU even split, against the VALU kernel's fixed 512-token
+// partitions.
+constexpr int kValuFixedPartition = 512;
+
+static bool even_valu_serves(int kv_dtype, int D, int H, int Hkv) {
+  return H == Hkv && (kv_dtype == HS_DTYPE_BF16 || kv_dtype == HS_DTYPE_F16) &&
+         (D == 32 || D == 64 || D == 128 || D == 256);
+}
+
+template <typename T>
+static const void* even_valu_kernel_t(int D) {
+  if (D == 32) return (const void*)row_attn_even_kernel<T, 32>;
+  if (D == 64) return (const void*)row_attn_even_kernel<T, 64>;
+  if (D == 128) return (const void*)row_attn_even_kernel<T, 128>;
+  return (const void*)row_attn_even_kernel<T, 256>;
+}
+
+static const void* even_valu_kernel(int kv_dtype, int D) {
+  return kv_dtype == HS_DTYPE_F16 ? even_valu_kernel_t<_Float16>(D) : even_valu_kernel_t<Bf16>(D);
+}
+
 // Resident workgroups of the kernel per CU and the CU count, on the current
 // device; looked up once per (device, kernel).
 static void even_occupancy(const void* fn, int block, int* occ, int* cus) {
@@ -875,12 +956,22 @@ static void even_occupancy(const void* fn, int block, int* occ, int* cus) {
 // bound on the real count, at most M partitions per unit).
 int splitmm_even_groups(int kv_dtype, int D, int H, int Hkv, int B, int MB) {
   const int G = H / Hkv;
-  if (!splitmm_serves(kv_dtype, kPage, D, H, Hkv) || G > kEvenMaxGroup) return 0;
   int occ = 0, cus = 0;
-  even_occupancy(even_kernel(kv_dtype, D), 64 * kEvenWaves, &occ, &cus);
+  int64_t groups, part;   // workgroups sharing a range; the fixed plan's partition
+  if (even_valu_serves(kv_dtype, D, H, Hkv)) {
+    even_occupancy(even_valu_kernel(kv_dtype, D), 64 * kEvenValuWaves, &occ, &cus);
+    groups = ceil_div(H, kEvenValuWaves);
+    part = kValuFixedPartition;
+  } else if (splitmm_serves(kv_dtype, kPage, D, H, Hkv) && G <= kEvenMaxGroup) {
+    even_occupancy(even_kernel(kv_dtype, D), 64 * kEvenWaves, &occ, &cus);
+    groups = Hkv;
+    part = splitmm_default_partition(G, D);
+  } else {
+    return 0;
+  }
   if (occ <= 0 || cus <= 0) return 0;
-  const int64_t fill = ceil_div((int64_t)cus * occ * kEvenRounds, Hkv);
-  const int64_t parts = sat_mul(B, ceil_div((int64_t)MB * kPage, splitmm_default_partition(G, D)));
+  const int64_t fill = ceil_div((int64_t)cus * occ * kEvenRounds, groups);
+  const int64_t parts = sat_mul(B, ceil_div((int64_t)MB * kPage, part));
   if (parts <= fill) return 0;
   return (int)std::min<int64_t>(fill, 1 << 20);
 }
@@ -912,15 +1003,32 @@ static void launch_even_for(const RowAttnArgs& a, int D, hipStream_t stream) {
 // The even-split kernel, then the merge of the rows it cut (which also
 // zeroes rows without keys).  Needs a.rows == a.B (one query row per
 // sequence) and a.H / a.Hkv <= kEvenMaxGroup.
+template <typename T>
+static void launch_even_valu_for(const RowAttnArgs& a, int D, hipStream_t stream) {
+  const dim3 grid((unsigned)(ceil_div(a.H, kEvenValuWaves) * (int64_t)a.even_m)),
+      block(64 * kEvenValuWaves);
+  if (D == 32) hipLaunchKernelGGL((row_attn_even_kernel<T, 32>), grid, block, 0, stream, a);
+  else if (D == 64) hipLaunchKernelGGL((row_attn_even_kernel<T, 64>), grid, block, 0, stream, a);
+  else if (D == 128) hipLaunchKernelGGL((row_attn_even_kernel<T, 128>), grid, block, 0, stream, a);
+  else hipLaunchKernelGGL((row_attn_even_kernel<T, 256>), grid, block, 0, stream, a);
+}
+
 void launch_splitmm_even(const RowAttnArgs& a, int kv_dtype, int D, hipStream_t stream) {
   profile_begin(stream);
-  if (kv_dtype == HS_DTYPE_F16) launch_even_for<F16Ops>(a, D, stream);
-  else launch_even_for<Bf16Ops>(a, D, stream);
+  if (even_valu_serves(kv_dtype, D, a.H, a.Hkv)) {
+    if (kv_dtype == HS_DTYPE_F16) launch_even_valu_for<_Float16>(a, D, stream);
+    else launch_even_valu_for<Bf16>(a, D, stream);
+  } else if (kv_dtype == HS_DTYPE_F16) {
+    launch_even_for<F16Ops>(a, D, stream);
+  } else {
+    launch_even_for<Bf16Ops>(a, D, stream);
+  }
   profile_end(stream);
   const dim3 grid((unsigned)(((int64_t)a.B * a.H + 3) / 4)), block(256);
   if (D == 32) hipLaunchKernelGGL(even_merge_kernel<32>, grid, block, 0, stream, a);
   else if (D == 64) hipLaunchKernelGGL(even_merge_kernel<64>, grid, block, 0, stream, a);
-  else hipLaunchKernelGGL(even_merge_kernel<128>, grid, block, 0, stream, a);
+  else if (D == 128) hipLaunchKernelGGL(even_merge_kernel<128>, grid, block, 0, stream, a);
+  else hipLaunchKernelGGL(even_merge_kernel<256>, grid, block, 0, stream, a);
 }
 
 }  // namespace hs

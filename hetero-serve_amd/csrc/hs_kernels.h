@@ -23,7 +23,7 @@ struct RowAttnArgs {
   int B, H, Hkv, BS, MB, NB;
   int mode;               // 0 one pass, 1 fixed partitions, 2 num_splits slices,
                           // 3 one pass per workgroup, keys split over its waves,
-                          // 4 even split (grouped-query matrix-core decode)
+                          // 4 even split (16-bit caches, up to 4 query heads per KV head)
   int part_tokens;        // mode 1
   int splits;             // mode 2
   int P;                  // partition slots per (row, head) in the grid
@@ -116,9 +116,10 @@ int splitmm_waves(int G);                                            // waves pe
 int splitmm_default_partition(int G, int D);                         // tokens, before small-grid cuts
 int64_t splitmm_grid(const RowAttnArgs& a);
 void launch_splitmm_part(const RowAttnArgs& a, int kv_dtype, int D, hipStream_t stream);
-// Even split (mode 4) of the same kernel family: the workgroups per unit that
-// fill the device once (occupancy of the kernel that serves this geometry on
-// the current device), and the workspace its states take.
+// Even split (mode 4): the split-operand kernel for 2 to 4 query heads per KV
+// head, the VALU walk for plain multi-head attention.  The workgroups per
+// unit that fill the device once (occupancy of the kernel that serves this
+// geometry on the current device), and the workspace its states take.
 int splitmm_even_groups(int kv_dtype, int D, int H, int Hkv, int B, int MB);   // 0: not served
 int splitmm_even_min_pages();
 struct EvenLayout {

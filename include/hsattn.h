@@ -136,14 +136,16 @@ size_t hs_decode_workspace_bytes(int B, int H, int Hkv, int D, int BS, int MB, i
  *                covers is written directly, without the merge.
  *                Must be a multiple of 16.
  *                With num_splits == 0 and partition_tokens == 0, fp16 and
- *                bf16 caches with 16-token pages and 2 to 4 query heads per
+ *                bf16 caches with 16-token pages and 1 to 4 query heads per
  *                KV head take the even split instead where their default
  *                partitions would overflow one round of the device: all
  *                pages of the batch, rows laid end to end, cut into one
- *                equal range per resident workgroup of each KV head, then
- *                a merge of the rows cut across ranges.  Same function;
- *                results agree with the fixed partitions to the
- *                split-operand precision, not bit for bit.
+ *                equal range per resident workgroup of each KV head (of
+ *                each pair of heads without grouping), then a merge of the
+ *                rows cut across ranges.  Same function; results agree
+ *                with the fixed partitions to fp32 rounding (to the
+ *                split-operand precision for grouped heads), not bit for
+ *                bit.
  *   workspace    device scratch of hs_decode_workspace_bytes(...) bytes
  *                (may be NULL when that is 0).
  */

@@ -138,23 +138,25 @@ def test_noalloc_under_graph_capture():
 
 
 def test_noalloc_refuses_calls_beyond_its_scratch():
-    """512 sequences of up to 8192 tokens at 32 heads need 136 MB of partition
-    states, more than the fixed 64 MiB: HS_EWORKSPACE, nothing launched.  The
-    inputs have the declared sizes, so that a regression of the check fails
-    on the assertions rather than reading past the tensors."""
+    """512 sequences of up to 8192 tokens at 32 heads on an fp32 cache (fixed
+    512-token partitions; 16-bit caches take the even split, whose states are
+    far smaller) need 136 MB of partition states, more than the fixed 64 MiB:
+    HS_EWORKSPACE, nothing launched.  The inputs have the declared sizes, so
+    that a regression of the check fails on the assertions rather than
+    reading past the tensors."""
     from heteroserve import _hip
 
     lib = _hip.lib()
     B, H, D, MB = 512, 32, 128, 512
     assert lib.hs_decode_workspace_bytes(B, H, H, D, 16, MB, 0, 0) > (64 << 20)
     gen = torch.Generator(device=DEV).manual_seed(1)
-    kc = torch.randn((1, 16, H, D), generator=gen, device=DEV).to(torch.bfloat16)
-    vc = torch.randn((1, 16, H, D), generator=gen, device=DEV).to(torch.bfloat16)
+    kc = torch.randn((1, 16, H, D), generator=gen, device=DEV)
+    vc = torch.randn((1, 16, H, D), generator=gen, device=DEV)
     q = torch.randn((B, H, D), generator=gen, device=DEV)
     bt = torch.zeros((B, MB), dtype=torch.int32, device=DEV)      # every page is block 0
     ctx = torch.full((B,), MB * 16, dtype=torch.int32, device=DEV)
     out = torch.zeros((B, H, D), device=DEV)
-    rc = lib.hs_decode_noalloc(q.data_ptr(), kc.data_ptr(), vc.data_ptr(), 2, kc.shape[0],
+    rc = lib.hs_decode_noalloc(q.data_ptr(), kc.data_ptr(), vc.data_ptr(), 0, kc.shape[0],
                                bt.data_ptr(), ctx.data_ptr(), out.data_ptr(), B, H, H, D,
                                16, MB, 0.1, 0, 0, torch.cuda.current_stream().cuda_stream)
     assert rc == -4
