@@ -413,13 +413,22 @@ def test_gqa_matrix_core_table_edges():
     # 300 rows: the row scans run over several 64-row chunks; G = 2
     (16, 8, 64, torch.bfloat16,
      [int(x) for x in np.random.default_rng(4).integers(0, 2000, 300)], False),
+    # plain multi-head attention (the VALU walk): the same edge rows
+    (32, 32, 128, torch.bfloat16,
+     [0, 1, 15, 16, 17, 8000, 0, 2047, 33, 5000] + [int(x) for x in
+                                                    np.random.default_rng(5).integers(64, 4000, 54)],
+     True),
+    (16, 16, 64, torch.float16,
+     [int(x) for x in np.random.default_rng(6).integers(0, 2000, 300)], False),
+    (8, 8, 256, torch.bfloat16, [70000, 69999, 70001, 65536], False),
 ])
 def test_even_split_decode(H, Hkv, D, dtype, lens, edges):
-    """The default decomposition of the grouped-query matrix-core decode on
-    grids that fill the device (up to 4 query heads per KV head): all pages of
-    the batch cut into one equal range per workgroup, rows cut across ranges
-    merged afterwards.  Against the oracle to the split operands' tolerance,
-    against fixed 512-token partitions of the same kernel family, and
+    """The default decomposition of decode on 16-bit caches with up to 4
+    query heads per KV head, on grids that fill the device: all pages of the
+    batch cut into one equal range per workgroup, rows cut across ranges
+    merged afterwards (the split-operand matrix cores for grouped heads, the
+    VALU walk for plain multi-head attention).  Against the oracle to the
+    split operands' tolerance, against fixed 512-token partitions, and
     bit-identical on a rerun; rows without keys are zero."""
     from heteroserve import _hip
 

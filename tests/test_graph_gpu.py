@@ -93,11 +93,13 @@ def test_decode_prefill_and_pack_replay_bit_exact():
                    [want_dec, want_gqa, want_g16, want_pre, want_pack])
 
 
-def test_even_split_decode_replays_bit_exact():
-    """The grouped-query decode's even split (4 query heads per KV head, a
-    batch whose fixed partitions would overflow one round of the device):
-    the even-split kernel and its merge, captured and replayed bit for bit,
-    and equal to the oracle-checked eager call."""
+@pytest.mark.parametrize("Hkv", [8, 32])
+def test_even_split_decode_replays_bit_exact(Hkv):
+    """The decode's even split (4 query heads per KV head on the matrix
+    cores, or plain multi-head attention on the VALU walk; a batch whose
+    fixed partitions would overflow one round of the device): the even-split
+    kernel and its merge, captured and replayed bit for bit, and equal to
+    the oracle-checked eager call."""
     from heteroserve import _hip
     from heteroserve.model import paged_attn
     from hsbench.cases import build_decode
@@ -105,7 +107,7 @@ def test_even_split_decode_replays_bit_exact():
     assert _hip.ready(), _hip.error()
     lens = np.random.default_rng(31).integers(64, 4000, 64)
     need = int(sum(-(-int(n) // 16) for n in lens))
-    case = build_decode("e", lens, 32, 8, 128, need + 64, torch.bfloat16, DEV, seed=31)
+    case = build_decode("e", lens, 32, Hkv, 128, need + 64, torch.bfloat16, DEV, seed=31)
     args = (case.q, case.k_cache, case.v_cache, case.block_tables, case.context_lens, case.scale)
     want = paged_attn.paged_attention(*args)
     fixed = _hip.decode(*args, 0, partition_tokens=768)
