@@ -1111,7 +1111,7 @@ def main() -> int:
         f"bytes={case.decode_bytes() / 1e9:.3f} GB")
     dec = decode_leg(case, args.steps, args.warmup, args.partition)
     log(f"decode: step {dec['step_ms'] * 1e3:.1f} us ({dec['step_gbs']:.0f} GB/s), "
-        f"partition kernel {dec['kernel_ms'] * 1e3:.1f} us ({dec['kernel_gbs']:.0f} GB/s)")
+        f"main kernel {dec['kernel_ms'] * 1e3:.1f} us ({dec['kernel_gbs']:.0f} GB/s)")
     cpu = None
     if with_cpu:
         cpu, outs = cpu_decode_baseline(case)
