@@ -14,7 +14,7 @@ def test_traffic_row_of_headline_kernel_is_found():
     # roofline.traffic comes from the committed rocprofv3 summary; the row
     # must exist for the kernel the headline leg runs, and the measured HBM
     # bytes must be close to the algorithmic K+V bytes of C2 (2.4617 GB)
-    traffic = bench.profiled_traffic(bench.DECODE_KERNEL, bench.DECODE_WORKGROUPS, "C2 alone")
+    traffic = bench.leg_traffic("C2")
     assert traffic is not None
     assert abs(traffic / 2_461_696_000 - 1.0) < 0.02
 
