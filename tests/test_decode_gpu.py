@@ -421,6 +421,9 @@ def test_gqa_matrix_core_table_edges():
     (16, 16, 64, torch.float16,
      [int(x) for x in np.random.default_rng(6).integers(0, 2000, 300)], False),
     (8, 8, 256, torch.bfloat16, [70000, 69999, 70001, 65536], False),
+    # an odd head count: the last two-head workgroup has one live wave
+    (5, 5, 128, torch.bfloat16,
+     [int(x) for x in np.random.default_rng(7).integers(1, 3000, 120)], False),
 ])
 def test_even_split_decode(H, Hkv, D, dtype, lens, edges):
     """The default decomposition of decode on 16-bit caches with up to 4
