@@ -510,6 +510,38 @@ def test_split_operand_decode_fuzz():
         assert _maxerr(got, want) <= SPLIT_TOL[dtype], (case, dtype, H, Hkv, D, lens, pt)
 
 
+def test_even_split_decode_fuzz():
+    """Seeded random batches through the default decomposition on grids large
+    enough for the even split: plain multi-head attention (the VALU walk) and
+    2 to 4 query heads per KV head (the split-operand matrix cores), bf16 and
+    fp16 caches, head dims 32 to 256, empty and clamped rows; each against
+    the oracle and against fixed partitions."""
+    from heteroserve import _hip
+
+    rng = np.random.default_rng(4242)
+    heads = [(32, 32), (16, 16), (12, 12), (32, 8), (16, 4), (24, 12), (8, 8), (20, 5)]
+    for case in range(10):
+        H, Hkv = heads[case % len(heads)]
+        dtype = (torch.bfloat16, torch.float16)[case % 2]
+        D = int(rng.choice([32, 64, 128, 256] if H == Hkv else [32, 64, 128]))
+        B = int(rng.integers(64, 260))
+        lens = [int(x) for x in rng.integers(0, 3000, size=B)]
+        pool, q, bt, ctx = _random_case(lens, H, Hkv, D, 16, dtype, seed=500 + case)
+        if case % 3 == 0:
+            ctx[1] = bt.shape[1] * 16 + 77      # clamped to the table
+            ctx[2] = -5                         # no keys
+        kp, vp = pool[0, 0], pool[0, 1]
+        scale = D ** -0.5
+        got = _hip.decode(q, kp, vp, bt, ctx, scale, 0)
+        want = _oracle(q, kp, vp, bt, ctx, scale)
+        live = (ctx > 0).cpu()
+        info = (case, dtype, H, Hkv, D, B)
+        assert _maxerr(got.cpu()[live], want[live]) <= SPLIT_TOL[dtype], info
+        assert torch.all(got.cpu()[~live] == 0), info
+        fixed = _hip.decode(q, kp, vp, bt, ctx, scale, 0, partition_tokens=512)
+        assert _maxerr(got, fixed) <= SPLIT_TOL[dtype], info
+
+
 def test_errors_are_raised_with_reference_messages():
     m1, m2, _ = _mods()
     pool, q, bt, ctx = _random_case([10], 4, 4, 64, 16, torch.float16, seed=1)
