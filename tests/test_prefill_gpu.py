@@ -303,3 +303,48 @@ def test_mfma_key_split_padded_rows():
     got = wm.paged_attention_prefill_wmma(q, pool[0, 0], pool[0, 1], bt, ctx, scale).cpu()
     assert torch.all(got[1, :22] == 0)
     assert _maxerr(got, _oracle(q, pool[0, 0], pool[0, 1], bt, ctx, scale)) <= 2e-3
+
+
+def test_prefill_fuzz():
+    """Seeded random ragged batches through hs_prefill_varlen: 1 to 40
+    sequences, prefixes up to 2500 tokens, chunks of 1 to 900 rows, head dims
+    32/64/128, 1 to 8 query heads per KV head, fp16 and bf16 caches.  The
+    shapes fall on every plan the matrix-core path has (the key-range split
+    and narrower workgroups of small grids, the grid kernel, the persistent
+    kernel of large ones); each runs with and without the workspace, and a
+    few sequences of each batch are checked against the oracle, 2e-3."""
+    from heteroserve import _hip
+    from hsbench.cases import build_prefill
+
+    _wmma()
+    rng = np.random.default_rng(777)
+    heads = [(32, 32), (32, 8), (16, 16), (16, 2), (8, 8), (24, 6), (64, 8), (8, 1)]
+    plans = set()
+    for case_no in range(12):
+        H, Hkv = heads[case_no % len(heads)]
+        D = int(rng.choice([32, 64, 128]))
+        dtype = (torch.float16, torch.bfloat16)[case_no % 2]
+        small = case_no % 3 == 0           # too few query tiles to cover the CUs
+        B = int(rng.integers(1, 7 if small else 41))
+        prefix = rng.integers(0, 2501, size=B)
+        chunk = rng.integers(1, (300 if small else 900) + 1, size=B)
+        need = int(sum(-(-int(p + s) // 16) for p, s in zip(prefix, chunk)))
+        case = build_prefill("fuzz", prefix, chunk, H, Hkv, D, need + 16, dtype, DEV,
+                             seed=900 + case_no)
+        ws = _hip.lib().hs_prefill_workspace_bytes(B, int(chunk.max()), H, D, 1)
+        plans.add("grid" if ws == 0 else "persistent" if ws == 256 else "key split")
+        cu = case.cu_seqlens.cpu().numpy()
+        kc, vc = case.k_cache.cpu(), case.v_cache.cpu()
+        seqs = sorted(set(int(b) for b in rng.choice(B, size=min(B, 4), replace=False)))
+        wants = {b: prefill_one(case.q[cu[b]:cu[b + 1]].cpu(), kc, vc,
+                                case.block_tables[b].cpu(), int(case.ctx[b]), case.scale)
+                 for b in seqs}
+        for split in (True, False):
+            got = _hip.prefill_varlen(case.q, case.cu_seqlens, int(chunk.max()), case.k_cache,
+                                      case.v_cache, case.block_tables, case.context_lens,
+                                      case.scale, use_mfma=True, split=split)
+            assert torch.isfinite(got).all(), (case_no, split)
+            for b in seqs:
+                err = _maxerr(got[cu[b]:cu[b + 1]], wants[b])
+                assert err <= 2e-3, (case_no, H, Hkv, D, dtype, B, split, b, err)
+    assert plans == {"grid", "persistent", "key split"}, plans
