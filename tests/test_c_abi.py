@@ -1,0 +1,45 @@
+"""The boundary from C: tests/c_abi/caller.c compiles against include/hsattn.h
+as C99 (-pedantic -Werror), links libhsattn.so and runs on a machine without
+a GPU (version check, workspace queries, argument errors as status codes)."""
+
+from __future__ import annotations
+
+import re
+import shutil
+import subprocess
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+CALLER = ROOT / "tests" / "c_abi" / "caller.c"
+HEADER = ROOT / "include" / "hsattn.h"
+
+
+def _declared_functions() -> set[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return set(re.findall(r"\b(hs_[a-z0-9_]+)\s*\(", text))
+
+
+def test_caller_takes_every_entry_point():
+    listed = set(re.findall(r"\(any_fn\)(hs_[a-z0-9_]+)", CALLER.read_text()))
+    assert listed == _declared_functions()
+
+
+def test_c_host_compiles_links_and_runs(tmp_path):
+    from heteroserve import _hip
+
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("no C compiler")
+    lib = _hip.lib_path()
+    if not lib.exists():
+        pytest.fail(f"{lib} missing: run python hetero-serve_amd/build.py")
+    exe = tmp_path / "caller"
+    subprocess.run([gcc, "-std=c99", "-pedantic", "-Wall", "-Wextra", "-Werror",
+                    f"-I{ROOT / 'include'}", str(CALLER), f"-L{lib.parent}", f"-l:{lib.name}",
+                    f"-Wl,-rpath,{lib.parent}", "-o", str(exe)], check=True,
+                   capture_output=True, text=True)
+    run = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
+    assert run.returncode == 0, run.stdout + run.stderr
+    assert run.stdout.strip().splitlines()[-1] == "OK", run.stdout
