@@ -43,3 +43,30 @@ def test_c_host_compiles_links_and_runs(tmp_path):
     run = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
     assert run.returncode == 0, run.stdout + run.stderr
     assert run.stdout.strip().splitlines()[-1] == "OK", run.stdout
+
+
+@pytest.mark.gpu
+def test_c_host_runs_decode_on_the_gpu(tmp_path):
+    """tests/c_abi/decode_gpu.c: a C host allocates and copies with the HIP
+    runtime's C API, calls hs_decode (default decomposition with its
+    workspace, and one pass) and checks the output against its own
+    double-precision decode of the same data, 1e-5 (fp32 cache)."""
+    from heteroserve import _hip
+
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("no C compiler")
+    rocm = Path("/opt/rocm")
+    lib = _hip.lib_path()
+    exe = tmp_path / "decode_gpu"
+    subprocess.run([gcc, "-std=c99", "-pedantic", "-Wall", "-Wextra", "-Werror",
+                    "-D__HIP_PLATFORM_AMD__", f"-I{ROOT / 'include'}", "-isystem",
+                    str(rocm / "include"), str(ROOT / "tests" / "c_abi" / "decode_gpu.c"),
+                    f"-L{lib.parent}", f"-l:{lib.name}", f"-L{rocm / 'lib'}", "-lamdhip64", "-lm",
+                    f"-Wl,-rpath,{lib.parent}", f"-Wl,-rpath,{rocm / 'lib'}", "-o", str(exe)],
+                   check=True, capture_output=True, text=True)
+    print("running", exe.name, flush=True)
+    run = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
+    print(run.stdout, flush=True)
+    assert run.returncode == 0, run.stdout + run.stderr
+    assert run.stdout.strip().splitlines()[-1] == "OK", run.stdout
