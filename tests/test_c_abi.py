@@ -1,6 +1,8 @@
-"""The boundary from C: tests/c_abi/caller.c compiles against include/hsattn.h
+"""The boundary from C.  tests/c_abi/caller.c compiles against include/hsattn.h
 as C99 (-pedantic -Werror), links libhsattn.so and runs on a machine without
-a GPU (version check, workspace queries, argument errors as status codes)."""
+a GPU (version check, workspace queries, argument errors as status codes);
+decode_gpu.c and pack_gpu.c run decode and a block migration on the GPU from
+C (the gpu-marked test)."""
 
 from __future__ import annotations
 
@@ -46,11 +48,13 @@ def test_c_host_compiles_links_and_runs(tmp_path):
 
 
 @pytest.mark.gpu
-def test_c_host_runs_decode_on_the_gpu(tmp_path):
-    """tests/c_abi/decode_gpu.c: a C host allocates and copies with the HIP
-    runtime's C API, calls hs_decode (default decomposition with its
-    workspace, and one pass) and checks the output against its own
-    double-precision decode of the same data, 1e-5 (fp32 cache)."""
+@pytest.mark.parametrize("program", ["decode_gpu", "pack_gpu"])
+def test_c_host_runs_on_the_gpu(program, tmp_path):
+    """C hosts that allocate and copy with the HIP runtime's C API and call
+    the library: decode_gpu.c runs hs_decode (default decomposition with its
+    workspace, and one pass) against its own double-precision decode of the
+    same data, 1e-5 (fp32 cache); pack_gpu.c packs scattered blocks of a
+    3-layer pool and unpacks them into another pool, byte for byte."""
     from heteroserve import _hip
 
     gcc = shutil.which("gcc")
@@ -58,10 +62,10 @@ def test_c_host_runs_decode_on_the_gpu(tmp_path):
         pytest.skip("no C compiler")
     rocm = Path("/opt/rocm")
     lib = _hip.lib_path()
-    exe = tmp_path / "decode_gpu"
+    exe = tmp_path / program
     subprocess.run([gcc, "-std=c99", "-pedantic", "-Wall", "-Wextra", "-Werror",
                     "-D__HIP_PLATFORM_AMD__", f"-I{ROOT / 'include'}", "-isystem",
-                    str(rocm / "include"), str(ROOT / "tests" / "c_abi" / "decode_gpu.c"),
+                    str(rocm / "include"), str(ROOT / "tests" / "c_abi" / f"{program}.c"),
                     f"-L{lib.parent}", f"-l:{lib.name}", f"-L{rocm / 'lib'}", "-lamdhip64", "-lm",
                     f"-Wl,-rpath,{lib.parent}", f"-Wl,-rpath,{rocm / 'lib'}", "-o", str(exe)],
                    check=True, capture_output=True, text=True)
