@@ -1,8 +1,8 @@
 """The boundary from C.  tests/c_abi/caller.c compiles against include/hsattn.h
 as C99 (-pedantic -Werror), links libhsattn.so and runs on a machine without
 a GPU (version check, workspace queries, argument errors as status codes);
-decode_gpu.c and pack_gpu.c run decode and a block migration on the GPU from
-C (the gpu-marked test)."""
+decode_gpu.c, prefill_gpu.c and pack_gpu.c run decode, chunked prefill and a
+block migration on the GPU from C (the gpu-marked test)."""
 
 from __future__ import annotations
 
@@ -48,13 +48,16 @@ def test_c_host_compiles_links_and_runs(tmp_path):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("program", ["decode_gpu", "pack_gpu"])
+@pytest.mark.parametrize("program", ["decode_gpu", "prefill_gpu", "pack_gpu"])
 def test_c_host_runs_on_the_gpu(program, tmp_path):
     """C hosts that allocate and copy with the HIP runtime's C API and call
     the library: decode_gpu.c runs hs_decode (default decomposition with its
     workspace, and one pass) against its own double-precision decode of the
-    same data, 1e-5 (fp32 cache); pack_gpu.c packs scattered blocks of a
-    3-layer pool and unpacks them into another pool, byte for byte."""
+    same data, 1e-5 (fp32 cache); prefill_gpu.c runs hs_prefill_varlen on
+    two ragged chunks over a bf16 cache, matrix cores within 2e-3 and the
+    fp32 row kernel within 1e-5 of its own double-precision prefill;
+    pack_gpu.c packs scattered blocks of a 3-layer pool and unpacks them into
+    another pool, byte for byte."""
     from heteroserve import _hip
 
     gcc = shutil.which("gcc")
